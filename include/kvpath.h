@@ -22,7 +22,9 @@
  *                             compaction primitive this library adds, bit-exact page copies)
  *   kvpath_workspace_bytes    no counterpart (the reference allocates its scratch inside torch;
  *                             here the caller allocates it, so graph capture sees no allocation)
- *   kvpath_partition_tokens   no counterpart (the reference does not split a row's keys)
+ *   kvpath_split_plan         no counterpart in kelpie's op (it does not split a row's keys); the
+ *                             per-sequence split follows kernels/vendored/cuda/vllm_attention/
+ *                             triton_unified_attention.py:335-355
  */
 #ifndef KVPATH_H
 #define KVPATH_H
@@ -100,8 +102,9 @@ typedef struct kvpath_plan {
 /* Attention options: `window` > 0 keeps keys (pos - window, pos] (0: no window; negative is
  * refused with KVPATH_EINVAL); `sinks` is NULL or f32[H]
  * per-head sink logits (kernels/ops/paged_attention.py:215-240); `causal` = 0 lets every row
- * see its entry's whole context (the DFlash drafter). `partition_tokens` is the split-KV
- * partition length, a multiple of 32; 0 lets the library choose (kvpath_partition_tokens). */
+ * see its entry's whole context (the DFlash drafter). `partition_tokens` is a fixed split-KV
+ * partition length for every entry, a multiple of 32; 0 lets the library split each entry by its
+ * own length on the device (kvpath_split_plan). */
 typedef struct kvpath_attn_opts {
     int32_t window;
     const float* sinks;
@@ -145,24 +148,36 @@ int32_t kvpath_copy_blocks(const kvpath_cache* cache, const int32_t* src, const 
                            int64_t n_pairs, kvpath_stream_t stream);
 
 /*
- * The split-KV partition length (keys) the library picks when kvpath_attn_opts.partition_tokens
- * is 0, for a step of num_tokens rows over num_reqs entries.  No counterpart in the reference
- * (its op attends each row in one pass): from 512 keys, longer for long tables and
- * prefill-sized steps, shortened to make the partition count odd; never below 384.
+ * How kvpath_attend splits a step's keys into split-KV partitions (no counterpart in kelpie's op,
+ * which attends each row in one pass).  With partition_tokens 0 the library chooses from the
+ * step's shape: each entry's keys (from its anchor: key 0, or with a window its first visible
+ * key rounded down to 32) are cut on the device, from its own seq_len, into
+ * min(slots, ceil(span / partition_tokens)) partitions of equal length rounded up to 32 keys, so
+ * the split does not depend on how wide the block table is beyond the slots an entry could fill
+ * (kelpie sizes tables for max_seq_len).  With partition_tokens > 0 (a multiple of 32) every
+ * partition has that length and slots = ceil(table_width * block / partition_tokens).
  */
-int32_t kvpath_partition_tokens(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
-                                int64_t kv_heads, int64_t table_width, int64_t block_size);
+typedef struct kvpath_split {
+    int32_t partition_tokens; /* per_entry: the floor of each entry's length; else every one's */
+    int32_t slots;            /* partitions per entry at most: the workspace's partition dim */
+    int32_t per_entry;        /* 1: sized per entry on the device; 0: fixed length */
+} kvpath_split;
+
+int32_t kvpath_split_plan(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
+                          int64_t kv_heads, int64_t table_width, int64_t block_size,
+                          int32_t partition_tokens, kvpath_split* out);
 
 /*
- * Scratch bytes kvpath_attend / kvpath_paged_attention need for a step of this shape (the
- * split-KV partials: per row, q head and partition, D values and 2 floats; sized for f32
- * values, which a bf16 q halves in use).  partition_tokens 0 gives a size that covers the
- * library's choice for any step of this shape.  -1 for a shape the library refuses: a negative
- * size, num_tokens / table_width / block_size of 2^31 or more (or a table spanning 2^31 keys),
- * more than 2^16 heads or head dims, a partition that is not a multiple of 32.
+ * Scratch bytes kvpath_attend / kvpath_paged_attention need for a step of this shape and
+ * partition_tokens (the split-KV partials: per row, q head and partition slot, D values and 2
+ * floats; sized for f32 values, which a bf16 q halves in use).  -1 for a shape the library
+ * refuses: a negative size, num_tokens / table_width / block_size of 2^31 or more (or a table
+ * spanning 2^31 keys), more than 65535 entries, more than 2^16 heads or head dims, q heads not a
+ * multiple of kv heads, a partition that is not a multiple of 32.
  */
-int64_t kvpath_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
-                               int64_t table_width, int64_t block_size, int32_t partition_tokens);
+int64_t kvpath_workspace_bytes(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
+                               int64_t kv_heads, int64_t head_dim, int64_t table_width,
+                               int64_t block_size, int32_t partition_tokens);
 
 /*
  * Attention only (replaces _attend and its mask/softmax, kernels/ops/paged_attention.py:
@@ -178,8 +193,8 @@ int32_t kvpath_attend(const kvpath_rows* q, const kvpath_cache* cache, const kvp
 /*
  * The two halves of kvpath_attend, for callers that schedule or time them apart (same
  * arguments; the partitions half does not read `out`).
- *   kvpath_attend_partitions  split-KV pass: for every row, q head and partition of
- *                             partition_tokens keys, the partial (o[D], max, sum) into
+ *   kvpath_attend_partitions  split-KV pass: for every row, q head and partition (as
+ *                             kvpath_split_plan describes), the partial (o[D], max, sum) into
  *                             `workspace`; with a bf16 q, o is normalized by the partition's sum
  *                             and stored in bf16 (as vLLM's paged_attention_v2 keeps its
  *                             partials), else un-normalized f32 (vLLM's segment kernel,

@@ -14,13 +14,25 @@
  *                            m * 2^-9, 0x7f NaN); pinned against torch's float8_e4m3fn cast.
  *   oracle_kv_append_fp8     the library's quantize-on-append rule (no reference counterpart):
  *                            per page a step touches and per (member, kv head), grouped by page
- *                            as a set of rows,
+ *                            as a set of rows, with t = absmax(rows) / 448,
  *                              fresh = the step writes the page's row 0
- *                              s_old = fresh ? 0 : scale;  s_new = max(s_old, absmax / 448)
- *                              if !fresh && s_old > 0 && s_new > s_old: every row the step does
- *                                not write becomes e4m3(clamp(f32(q) * s_old / s_new, +-448))
- *                              each written row becomes e4m3(clamp(x / s_new, +-448)) (0 when
- *                                s_new == 0); scale = s_new.
+ *                              s_old = fresh ? 0 : scale
+ *                              s_new = t                    when s_old == 0
+ *                                      s_old * 2^k          when t > s_old > 0, k >= 1 the
+ *                                                           smallest with s_old * 2^k >= t
+ *                                      s_old                otherwise
+ *                              r_new = 1 / s_new (0 when s_new == 0)
+ *                              if k > 0: every row the step does not write becomes
+ *                                e4m3(clamp(f32(q) * 2^-k, +-448)), exact unless it falls below
+ *                                e4m3's normals (the clamp only turns a stale NaN byte into -448)
+ *                              each written row becomes e4m3(clamp(x * r_new, +-448));
+ *                              scale = s_new.
+ *                            A fresh page's largest element is stored exactly (it maps to 448);
+ *                            a scale only ever grows by a power of two, so requantizing the rows
+ *                            already in a page is an exponent shift and the e4m3 rounding does not
+ *                            compound over a decode stream. One reciprocal per (page, member,
+ *                            head), then a product per value (the form vLLM's scaled fp8
+ *                            quantization uses).
  * Floating point here is IEEE binary32, one rounding per operation (built with
  * -ffp-contract=off, no fast-math). Strides are in elements; offsets are 64-bit.
  */
@@ -83,9 +95,19 @@ void oracle_e4m3_decode_array(const uint8_t* q, float* out, int64_t n) {
 
 static float clamp448(float x) { return fminf(fmaxf(x, -448.0f), 448.0f); }
 
-uint8_t oracle_fp8_quantize(float x, float scale) {
-    if (!(scale > 0.0f)) return 0;
-    return oracle_e4m3_encode(clamp448(x / scale));
+/* x quantized against a page scale s through its reciprocal r = 1 / s (r == 0: s == 0). */
+uint8_t oracle_fp8_quantize(float x, float r) {
+    if (!(r > 0.0f)) return 0;
+    return oracle_e4m3_encode(clamp448(x * r));
+}
+
+float oracle_fp8_reciprocal(float s) { return s > 0.0f ? 1.0f / s : 0.0f; }
+
+/* The smallest k >= 1 with s_old * 2^k >= t (t > s_old > 0), by exact power-of-two products. */
+int oracle_fp8_growth(float s_old, float t) {
+    int k = 1;
+    while (ldexpf(s_old, k) < t) ++k;
+    return k;
 }
 
 /* ---- same-dtype append, gather, copy ------------------------------------------------------ */
@@ -175,22 +197,23 @@ void oracle_kv_append_fp8(ocache* c, const float* k, const float* v, int64_t k_s
                 }
                 float* scale = c->scale + (page * 2 + m) * c->hkv + h;
                 const float s_old = fresh ? 0.0f : *scale;
-                const float s_new = fmaxf(s_old, amax / 448.0f);
-                if (!fresh && s_old > 0.0f && s_new > s_old) {
+                const float t_new = amax / 448.0f;
+                const int k = (s_old > 0.0f && t_new > s_old) ? oracle_fp8_growth(s_old, t_new) : 0;
+                const float s_new = s_old > 0.0f ? ldexpf(s_old, k) : t_new;
+                const float r_new = oracle_fp8_reciprocal(s_new);
+                if (k > 0) {
                     for (int64_t row = 0; row < c->block; ++row) {
                         if (written[row]) continue;
                         uint8_t* q = c->base + elem_offset(c, page, m, row, h);
-                        for (int64_t d = 0; d < c->d; ++d) {
-                            const float x = (oracle_e4m3_decode(q[d]) * s_old) / s_new;
-                            q[d] = oracle_e4m3_encode(clamp448(x));
-                        }
+                        for (int64_t d = 0; d < c->d; ++d)
+                            q[d] = oracle_e4m3_encode(clamp448(ldexpf(oracle_e4m3_decode(q[d]), -k)));
                     }
                 }
                 for (int64_t t = t0; t < T; ++t) {
                     if (slots[t] < 0 || slots[t] >= pool || slots[t] / c->block != page) continue;
                     uint8_t* q = c->base + elem_offset(c, page, m, slots[t] % c->block, h);
                     for (int64_t d = 0; d < c->d; ++d)
-                        q[d] = oracle_fp8_quantize(src[t * srow + h * shead + d], s_new);
+                        q[d] = oracle_fp8_quantize(src[t * srow + h * shead + d], r_new);
                 }
                 *scale = s_new;
             }

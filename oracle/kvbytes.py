@@ -92,8 +92,9 @@ def e4m3_decode(q: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def fp8_quantize(x: float, scale: float) -> int:
-    return int(load().oracle_fp8_quantize(x, scale))
+def fp8_quantize(x: float, reciprocal: float) -> int:
+    """x quantized against a page scale s through its reciprocal r = 1 / s (0: s == 0)."""
+    return int(load().oracle_fp8_quantize(x, reciprocal))
 
 
 def kv_append(kv_member: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

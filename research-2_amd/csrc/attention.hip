@@ -50,6 +50,7 @@ constexpr float kNegInf = -__builtin_huge_valf();
 
 struct Entry {
     int32_t q0, n_rows, seq_len, n_q;  // first row, rows, context length (clamped), q-rows
+    int32_t anchor, part;              // partition 0's first key, partition length (split_entry)
 };
 
 // r must be in [0, R). All three scalars are loaded before any test, so they travel together
@@ -120,15 +121,28 @@ __device__ __forceinline__ WgCoord work_coord(const AttnArgs& a) {
 // then start at partition 0, so the grid holds only as many partitions as a window can reach
 // (one, when it fits a partition: decode then writes its output directly), and a long context
 // adds no workgroups that find nothing to do.
-__device__ __forceinline__ int part_anchor(const AttnArgs& a, const Entry& e) {
-    return a.window > 0 ? max(0, e.seq_len - e.n_rows - a.window + 1) / 32 * 32 : 0;
+//
+// The partition length is the step's fixed length (a.part_fixed: a caller's explicit choice), or
+// each entry's own split of its span (keys from the anchor to the end of its context), decided
+// here from its seq_len alone: ceil(span / a.part) partitions (a.part is the floor length), at
+// most the grid's slots per entry, of equal 32-key-aligned length. A short entry then takes few
+// slots and a long one all of them, whatever the block table's width (kelpie sizes it for
+// max_seq_len: kelpie-core/src/scheduler.zig:1577-1578), as the reference design point splits
+// each sequence by its own length under a fixed grid (kernels/vendored/cuda/vllm_attention/
+// triton_unified_attention.py:335-355).
+__device__ __forceinline__ void split_entry(const AttnArgs& a, Entry& e) {
+    e.anchor = a.window > 0 ? max(0, e.seq_len - e.n_rows - a.window + 1) / 32 * 32 : 0;
+    if (a.part_fixed) {
+        e.part = a.part;
+        return;
+    }
+    const int span = e.seq_len - e.anchor;
+    const int n = min(max((span + a.part - 1) / a.part, 1), a.grid_parts);
+    e.part = ((span + n - 1) / n + 31) / 32 * 32;
 }
 
-// The partition a workgroup serves is its slot (blockIdx.x = slot + grid_parts * tg up to the
-// rotation above); its first key:
-__device__ __forceinline__ int part_start(const AttnArgs& a, const Entry& e, int p) {
-    return part_anchor(a, e) + p * a.part;
-}
+// The first key of partition p of a split entry.
+__device__ __forceinline__ int part_start(const Entry& e, int p) { return e.anchor + p * e.part; }
 
 // Keys [lo, hi) some q-row in [qr0, qr1) of the entry can see.
 __device__ __forceinline__ void visible_span(const AttnArgs& a, const Entry& e, int qr0, int qr1,
@@ -542,8 +556,9 @@ __device__ __forceinline__ void partition_body(const AttnArgs& a, char* lds) {
 
     Entry e;
     if (!load_entry(a, r, e)) return;
+    split_entry(a, e);
     const int p = p_rel;
-    const int part_lo = part_start(a, e, p);
+    const int part_lo = part_start(e, p);
     if (part_lo >= e.seq_len) return;
     // The page ids of this wave's first 32 blocks when its keys start at the partition's first
     // key (always so without a window), loaded right after the entry's scalars, before anything
@@ -557,7 +572,7 @@ __device__ __forceinline__ void partition_body(const AttnArgs& a, char* lds) {
         const int64_t pi = ((spec_kb0 + kWaves * (lane >> 1)) * 32 + (lane & 1) * 16) / block;
         if (pi < a.table_width) spec_pid = a.table[table_row + pi];
     }
-    const int part_hi = min(part_lo + a.part, e.seq_len);
+    const int part_hi = min(part_lo + e.part, e.seq_len);
 
     const char* cache = static_cast<const char*>(a.c.base);
     const int64_t head_bytes = static_cast<int64_t>(h) * a.c.s_head * ES;
@@ -1106,10 +1121,11 @@ void attn_partition_verify(AttnArgs a) {
     const int tg0 = static_cast<int>(wc.x) / a.grid_parts;
     Entry e;
     if (!load_entry(a, r, e)) return;
+    split_entry(a, e);
     const int p = part_slot(a, wc.x, wc.y, wc.z);
-    const int part_lo = part_start(a, e, p);
+    const int part_lo = part_start(e, p);
     if (part_lo >= e.seq_len) return;
-    const int part_hi = min(part_lo + a.part, e.seq_len);
+    const int part_hi = min(part_lo + e.part, e.seq_len);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -1460,10 +1476,11 @@ __global__ __launch_bounds__(kThreads) void attn_partition_generic(AttnArgs a) {
     const int tg = blockIdx.x / a.grid_parts;
     Entry e;
     if (!load_entry(a, r, e)) return;
+    split_entry(a, e);
     const int p = part_slot(a);
-    const int part_lo = part_start(a, e, p);
+    const int part_lo = part_start(e, p);
     if (part_lo >= e.seq_len) return;
-    const int part_hi = min(part_lo + a.part, e.seq_len);
+    const int part_hi = min(part_lo + e.part, e.seq_len);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int D = a.c.d;
     constexpr int kPer = kGenMaxD / 64;
@@ -1566,9 +1583,9 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce(AttnArgs a) {
         const int qrow = (t - e.q0) * a.G;
         visible_span(a, e, qrow, qrow + 1, lo, hi);
         hi = min(hi, e.seq_len);
-        const int anchor = part_anchor(a, e);
-        p_lo = (lo - anchor) / a.part;
-        p_hi = (hi - 1 - anchor) / a.part;
+        split_entry(a, e);
+        p_lo = (lo - e.anchor) / e.part;
+        p_hi = (hi - 1 - e.anchor) / e.part;
     }
 
     const int64_t out_base = static_cast<int64_t>(t) * a.out_srow + static_cast<int64_t>(hq) * a.out_shead;
@@ -1703,8 +1720,8 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce_few(AttnArgs a) {
         const int qrow = (t - e.q0) * a.G;
         visible_span(a, e, qrow, qrow + 1, lo, hi);
         hi = min(hi, e.seq_len);
-        const int anchor = part_anchor(a, e);
-        const int p_lo = (lo - anchor) / a.part, n_p = (hi - 1 - anchor) / a.part - p_lo + 1;
+        split_entry(a, e);
+        const int p_lo = (lo - e.anchor) / e.part, n_p = (hi - 1 - e.anchor) / e.part - p_lo + 1;
         // Every (m, l) and partial load is issued before one wait: slots past n_p re-read slot
         // p_lo (L1 hits) and are masked after the loads. The loads are inline asm the compiler
         // does not track (it would otherwise wait for the maxima before issuing the partials).
@@ -1837,50 +1854,56 @@ int64_t tile_groups_for(int64_t tiles) { return tiles <= 1 ? 1 : std::min<int64_
 
 }  // namespace
 
-int32_t choose_partition(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int64_t kv_heads,
-                         int64_t width, int64_t block) {
+SplitChoice choose_split(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int64_t kv_heads,
+                         int64_t width, int64_t block, int32_t partition) {
+    const int64_t keys = width * block;
+    const auto cdiv = [](int64_t x, int64_t y) { return (x + y - 1) / y; };
+    if (partition > 0)  // the caller's length, every entry alike
+        return SplitChoice{partition, static_cast<int32_t>(std::max<int64_t>(1, cdiv(keys, partition))), 1};
     constexpr int32_t kBase = 512;
-    if (n_tokens <= 0 || n_reqs <= 0 || kv_heads <= 0 || width <= 0 || block <= 0) return kBase;
+    if (n_tokens <= 0 || n_reqs <= 0 || kv_heads <= 0 || width <= 0 || block <= 0)
+        return SplitChoice{kBase, 1, 0};
     const int64_t tiles = tiles_per_entry(n_tokens, n_reqs, q_heads / kv_heads);
     const int64_t groups = tile_groups_for(tiles);
-    // Every partition a workgroup serves costs a fixed start (entry and table loads before its
-    // first K/V bytes) and end (partial stores, whose HBM writes interleaved with the K/V stream
-    // cost far more per byte than the reads); longer partitions amortize both, fewer
-    // workgroups balance worse. Measured on MI355X:
-    //  - decode steps double from 512 keys while the table still splits into 8+ partitions and
-    //    the grid keeps 2048+ workgroups (64 entries of 1-4k keys: 512; 128 entries of 2-8k
-    //    keys: 1024; 4 entries of 128k: 2048);
-    //  - multi-row steps of one row group per entry (verify, drafter) write a partial per row
-    //    and double while the grid keeps 1024+ workgroups and 8+ partitions (16 entries of 16
-    //    rows over 0.5-8k keys: 1024; over six length draws 512 keys averaged 89.3 us a step,
-    //    800-1000 keys 85.0-85.7);
-    //  - prefill-sized steps (8+ workgroups per partition from their rows alone) double while
-    //    the grid keeps 1024+ workgroups (four per CU), which also saves each workgroup's q load.
-    const int64_t keys = width * block;
+    // Each entry is split on the device by its own length (split_entry): ceil(span / base)
+    // partitions of equal length, at most `slots` of them. The slots bound the grid
+    // (R x Hkv x tile groups x slots workgroups, the empty ones retire at once) and the
+    // workspace; they are chosen from the step's shape, never from how wide the block table is
+    // beyond what one entry could fill at the floor length. Every partition a workgroup serves
+    // costs a fixed start (entry and table loads before its first K/V bytes) and end (partial
+    // stores, whose HBM writes interleaved with the K/V stream cost far more per byte than the
+    // reads); longer partitions amortize both, fewer workgroups balance worse. Measured on
+    // MI355X:
+    //  - decode: 512-key floor, slots for 2048+ workgroups over the grid and at least nine (64
+    //    entries of 1-4k keys: partitions of <= 512 keys, nine slots; 4 entries of 128k: 65
+    //    slots of 2048 keys);
+    //  - multi-row steps of one row group per entry (verify, drafter) write a partial per row:
+    //    896-key floor (16 entries of 16 rows over 0.5-8k keys: 512-key partitions averaged
+    //    89.3 us a step, 800-1000 keys 85.0-85.7), slots for 1024+ workgroups, at least nine;
+    //  - prefill-sized steps (8+ workgroups per partition from their rows alone) fill the grid
+    //    with rows: slots only up to 1024 workgroups (4 x 512-row chunks after 2k keys: one
+    //    partition, 124 us, against 155-176 us split).
+    // An odd slot count keeps the grid's x extent odd, which spreads each entry's partitions
+    // over consecutive XCDs (part_slot).
     const int64_t wgs = n_reqs * kv_heads * groups;
     const bool prefill = groups >= 8;
     const bool multi_row = tiles > 1;
-    const auto parts_of = [keys](int64_t p) { return (keys + p - 1) / p; };
-    int64_t part = kBase;
-    while (part < keys && part < (1 << 20)) {
-        const int64_t next = part * 2;
-        const int64_t parts = parts_of(next);
-        if (prefill ? wgs * parts < 1024
-                    : (parts < 8 || wgs * parts < (multi_row ? 1024 : 2048))) break;
-        part = next;
-    }
-    // An odd partition count keeps the grid's x extent odd (see part_slot): 64-entry decode at 4096 keys
-    // runs 114 us with 480-key partitions (9) against 120 us with 512-key ones (8). Shrink by
-    // 32-key steps, to no less than three quarters, until the count is odd.
-    if (parts_of(part) > 1 && parts_of(part) % 2 == 0) {
-        for (int64_t q = part - 32; q >= part * 3 / 4; q -= 32) {
-            if (parts_of(q) % 2 == 1) {
-                part = q;
-                break;
-            }
-        }
-    }
-    return static_cast<int32_t>(part);
+    const int64_t base = prefill ? 512 : (multi_row ? 896 : kBase);
+    int64_t cap = prefill ? std::max<int64_t>(1, 1024 / wgs)
+                          : std::max<int64_t>(9, cdiv(multi_row ? 1024 : 2048, wgs));
+    if (cap > 1 && cap % 2 == 0) cap += 1;
+    const int64_t slots = std::min<int64_t>(cap, std::max<int64_t>(1, cdiv(keys, base)));
+    return SplitChoice{static_cast<int32_t>(base), static_cast<int32_t>(slots), 0};
+}
+
+int32_t grid_slots(int32_t window, int64_t n_tokens, int32_t part, int32_t slots) {
+    // With a window, an entry's visible keys span at most window + rows - 1 keys (rows <= T)
+    // from its anchor's block, so at most window + T + 30 keys from the anchor; a split entry's
+    // span from its anchor is at most that many keys too, so its share of the floor length
+    // needs no more slots either.
+    if (window <= 0) return slots;
+    return static_cast<int32_t>(
+        std::min<int64_t>(slots, (static_cast<int64_t>(window) + n_tokens + 30 + part - 1) / part));
 }
 
 // Row tiles per entry from which a bf16 multi-row step takes two tiles per wave.
@@ -1898,11 +1921,6 @@ void partition_shape(AttnArgs& a, int& nt, dim3& grid) {
     // Multi-row steps: a workgroup takes nt row tiles; long steps (prefill) spread the rest
     // over more workgroups, each reading the partition's K/V again (from L2 when they share it).
     a.tile_groups = nt > 1 ? static_cast<int>(std::min<int64_t>(64, (tiles + nt - 1) / nt)) : 1;
-    // With a window, an entry's visible keys span at most window + rows - 1 keys (rows <= T)
-    // from its anchor's block, so at most window + T + 30 keys from the anchor.
-    a.grid_parts = a.window > 0
-        ? static_cast<int>(std::min<int64_t>(a.n_parts, (static_cast<int64_t>(a.window) + a.T + 30 + a.part - 1) / a.part))
-        : a.n_parts;
     grid = dim3(static_cast<unsigned>(a.grid_parts * a.tile_groups), static_cast<unsigned>(a.c.hkv),
                 static_cast<unsigned>(a.R));
 }

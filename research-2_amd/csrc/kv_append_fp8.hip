@@ -4,21 +4,38 @@
 // is the library's own rule, chosen so the result does not depend on the order of a step's rows:
 //   1. The rows of one step that land in one page form a run of consecutive rows (an entry's
 //      rows are its newest positions, in order); the run's first row is its leader.
-//   2. For each (member m in {K, V}, kv head h) of the page:
+//   2. For each (member m in {K, V}, kv head h) of the page, with t = absmax(run rows) / 448:
 //        fresh  = the run writes the page's row 0 (a page is always filled from row 0, so the
 //                 old scale and rows belong to a previous owner and are discarded)
 //        s_old  = fresh ? 0 : scale[page, m, h]
-//        s_new  = max(s_old, absmax(run rows) / 448)
-//      If s_new > s_old > 0, every row of the page the run does not write is requantized:
-//        q' = e4m3(clamp(f32(q) * s_old / s_new, +-448)).
-//      Each run row is quantized as q = e4m3(clamp(x / s_new, +-448)) (q = 0 when s_new = 0),
-//      and scale[page, m, h] = s_new.
+//        s_new  = t when s_old = 0; s_old * 2^k when t > s_old > 0, k >= 1 the smallest with
+//                 s_old * 2^k >= t; s_old otherwise
+//        r_new  = 1 / s_new (0 when s_new = 0)
+//      When the scale grew (k > 0), every row of the page the run does not write is requantized
+//      as q' = e4m3(clamp(f32(q) * 2^-k, +-448)) -- an exponent shift, exact unless the value
+//      drops below e4m3's normals. Each run row is quantized as q = e4m3(clamp(x * r_new,
+//      +-448)), and scale[page, m, h] = s_new.
+// A fresh page's largest element maps to 448; growth by powers of two keeps the e4m3 rounding of
+// a decode stream (a row appended per step, the scale growing on many of them) from compounding.
 // Products and quotients are single IEEE-754 binary32 operations rounded to nearest even; the
-// e4m3 conversion rounds to nearest even.  Dequantized value = f32(q) * scale.
+// e4m3 conversion rounds to nearest even.  Dequantized value = f32(q) * scale.  One reciprocal
+// per (page, member, head) and a product per value (the form vLLM's scaled fp8 quantization
+// uses) keeps the per-value work to a multiply, a clamp and half a conversion instruction.
 //
-// One workgroup per row; only run leaders work.  A (member, head) pair is owned by a group of
-// 16 lanes, which computes its absmax with shuffles and then does all of its writes, so groups
-// never need to synchronize with each other.
+// append_fp8_runs (bf16 rows, D of 64, 128 or 256): a workgroup takes a chunk of consecutive
+// rows; each of them that leads a run becomes 2 * Hkv units (member, kv head), and the
+// workgroup's lane groups (D / 8 lanes: a lane owns 8 dims, 16 bytes of a bf16 row and 8 bytes of
+// its e4m3 row) take the units round-robin. A unit loads its run's rows (the first 16 kept in
+// registers, every load issued before the first use), reduces the absmax across its lanes,
+// requantizes the page's other rows when the scale grew, and stores the run's rows as packed
+// e4m3. Whole-page (prefill-shaped) appends take chunks of 16 rows, so each workgroup serves one
+// page of every (member, head); decode-shaped ones take one row per workgroup, so every
+// (row, member, head) unit runs in parallel.
+//
+// append_fp8_generic (any input dtype, any D or alignment): one workgroup per row, only run
+// leaders work; a (member, head) pair is owned by a group of 16 lanes.
+#include <algorithm>
+
 #include "kvpath_device.h"
 #include "kvpath_internal.h"
 
@@ -26,13 +43,202 @@ namespace kvpath {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kGroup = 16;  // lanes per (member, head)
 
 __device__ __forceinline__ int64_t page_of(int64_t slot, int64_t block, int64_t pool) {
     return (slot >= 0 && slot < pool) ? slot / block : -1;
 }
 
-__global__ __launch_bounds__(kThreads) void append_fp8(AppendArgs a) {
+// Two f32 as two e4m3 bytes in the low (hi_word false) or high half of `word`: clamp to
+// [-448, 448], then the hardware conversion (round to nearest even; the clamp keeps (448, 464]
+// and beyond from becoming NaN).
+template <bool HiWord>
+__device__ __forceinline__ int cvt2_fp8(float x, float y, int word) {
+    x = fminf(fmaxf(x, -kFp8Max), kFp8Max);
+    y = fminf(fmaxf(y, -kFp8Max), kFp8Max);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(x, y, word, HiWord);
+}
+
+// The scale rule for one (page, member, head): s_new and the growth exponent k from the stored
+// scale s_old (0 for a fresh page) and t = absmax / 448. Uniform across the lanes that call it.
+__device__ __forceinline__ float grow_scale(float s_old, float t, int& k) {
+    k = 0;
+    if (!(s_old > 0.0f)) return t;
+    if (!(t > s_old)) return s_old;
+    k = 1;
+    while (__builtin_amdgcn_ldexpf(s_old, k) < t) ++k;
+    return __builtin_amdgcn_ldexpf(s_old, k);
+}
+
+// Eight e4m3 values shifted down by 2^k, requantized (exact for values that stay normal).
+__device__ __forceinline__ u32x2 requant8(u32x2 q, int k) {
+    const f32x4 lo = fp8x4_to_f32(q[0]), hi = fp8x4_to_f32(q[1]);
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    int w0 = cvt2_fp8<false>(__builtin_amdgcn_ldexpf(x[0], -k), __builtin_amdgcn_ldexpf(x[1], -k), 0);
+    w0 = cvt2_fp8<true>(__builtin_amdgcn_ldexpf(x[2], -k), __builtin_amdgcn_ldexpf(x[3], -k), w0);
+    int w1 = cvt2_fp8<false>(__builtin_amdgcn_ldexpf(x[4], -k), __builtin_amdgcn_ldexpf(x[5], -k), 0);
+    w1 = cvt2_fp8<true>(__builtin_amdgcn_ldexpf(x[6], -k), __builtin_amdgcn_ldexpf(x[7], -k), w1);
+    return u32x2{static_cast<uint32_t>(w0), static_cast<uint32_t>(w1)};
+}
+
+// Eight values times r as eight e4m3 bytes.
+__device__ __forceinline__ u32x2 quantize8(const float (&x)[8], float r) {
+    int lo = cvt2_fp8<false>(x[0] * r, x[1] * r, 0);
+    lo = cvt2_fp8<true>(x[2] * r, x[3] * r, lo);
+    int hi = cvt2_fp8<false>(x[4] * r, x[5] * r, 0);
+    hi = cvt2_fp8<true>(x[6] * r, x[7] * r, hi);
+    return u32x2{static_cast<uint32_t>(lo), static_cast<uint32_t>(hi)};
+}
+
+// Eight bf16 (16 bytes) as eight f32, exact.
+__device__ __forceinline__ void widen_bf16x8(u32x4 w, float (&x)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ float absmax8(const float (&x)[8]) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(x[i]));
+    return m;
+}
+
+constexpr int kMaxChunk = 64;  // rows per workgroup at most
+constexpr int kWindow = kMaxChunk + 64;  // slots staged in LDS: the chunk and the runs it leads
+constexpr int kKeep = 16;  // run rows a unit keeps in registers between its two passes
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int chunk) {
+    constexpr int L = D / 8;             // lanes per unit
+    constexpr int G = kThreads / L;      // units in flight per workgroup
+    __shared__ int64_t s_slot[kWindow + 1];  // slots of rows c0 - 1 .. c0 + kWindow - 1
+    __shared__ int s_lead[kMaxChunk];
+    __shared__ int s_len[kMaxChunk];
+    __shared__ uint64_t s_written[kMaxChunk];
+    __shared__ int s_n;
+
+    const int64_t block = a.c.block;
+    const int64_t pool = a.c.num_pages * block;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int tid = static_cast<int>(threadIdx.x);
+    if (tid == 0) s_n = 0;
+    for (int i = tid; i < kWindow + 1; i += kThreads) {
+        const int64_t t = c0 - 1 + i;
+        s_slot[i] = (t >= 0 && t < a.T) ? static_cast<int64_t>(a.slots[t]) : -1;
+    }
+    __syncthreads();
+    // Leaders of this chunk, with their runs: the rows after them in the same page.
+    if (tid < chunk && c0 + tid < a.T) {
+        const int64_t slot = s_slot[tid + 1];
+        const int64_t page = page_of(slot, block, pool);
+        if (page >= 0 && page_of(s_slot[tid], block, pool) != page) {
+            uint64_t written = 1ull << (slot - page * block);
+            int n = 1;
+            for (;;) {
+                const int64_t t = c0 + tid + n;
+                if (t >= a.T) break;
+                const int w = tid + n + 1;
+                const int64_t s2 = w <= kWindow ? s_slot[w] : static_cast<int64_t>(a.slots[t]);
+                if (page_of(s2, block, pool) != page) break;
+                written |= 1ull << (s2 - page * block);
+                ++n;
+            }
+            const int at = atomicAdd(&s_n, 1);
+            s_lead[at] = static_cast<int>(c0 + tid);
+            s_len[at] = n;
+            s_written[at] = written;
+        }
+    }
+    __syncthreads();
+
+    const int hkv = a.c.hkv;
+    const int n_units = s_n * 2 * hkv;
+    const int grp = tid / L, lane = tid % L;
+    uint8_t* cache = static_cast<uint8_t*>(a.c.base);
+    for (int u = grp; u < n_units; u += G) {
+        const int li = u / (2 * hkv), pair = u - li * 2 * hkv;
+        const int m = pair / hkv, h = pair - m * hkv;
+        const int64_t t0 = s_lead[li];
+        const int n = s_len[li];
+        const uint64_t written = s_written[li];
+        const bool fresh = written & 1ull;
+        const int64_t page = static_cast<int64_t>(a.slots[t0]) / block;
+        const uint16_t* src = static_cast<const uint16_t*>(m ? a.v : a.k) +
+                              h * (m ? a.v_shead : a.k_shead) + 8 * lane;
+        const int64_t s_row = m ? a.v_srow : a.k_srow;
+        float* scale_slot = a.c.scale + (page * 2 + m) * hkv + h;
+        const int64_t head_base = page * a.c.s_page + m * a.c.s_kv + h * a.c.s_head + 8 * lane;
+
+        // Pass 1: the run's absmax; its first kKeep rows stay in registers.
+        u32x4 keep[kKeep];
+#pragma unroll
+        for (int j = 0; j < kKeep; ++j)
+            keep[j] = j < n ? *reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row) : u32x4{0, 0, 0, 0};
+        const float s_stored = *scale_slot;
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kKeep; ++j) {
+            float x[8];
+            widen_bf16x8(keep[j], x);
+            amax = fmaxf(amax, absmax8(x));
+        }
+        for (int j = kKeep; j < n; ++j) {
+            float x[8];
+            widen_bf16x8(*reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row), x);
+            amax = fmaxf(amax, absmax8(x));
+        }
+#pragma unroll
+        for (int o = L / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, L));
+
+        int k;
+        const float s_new = grow_scale(fresh ? 0.0f : s_stored, __fdiv_rn(amax, kFp8Max), k);
+        const float r_new = s_new > 0.0f ? __fdiv_rn(1.0f, s_new) : 0.0f;
+
+        // The page's other rows, when the scale grew: f32(q) * 2^-k, requantized.
+        if (k > 0) {
+            for (int64_t row0 = 0; row0 < block; row0 += kKeep) {
+                u32x2 q[kKeep];
+#pragma unroll
+                for (int j = 0; j < kKeep; ++j) {
+                    const int64_t row = row0 + j;
+                    q[j] = row < block && !(written >> row & 1ull)
+                               ? *reinterpret_cast<const u32x2*>(cache + head_base + row * a.c.s_row)
+                               : u32x2{0, 0};
+                }
+#pragma unroll
+                for (int j = 0; j < kKeep; ++j) {
+                    const int64_t row = row0 + j;
+                    if (row >= block || (written >> row & 1ull)) continue;
+                    *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) = requant8(q[j], k);
+                }
+            }
+        }
+
+        // Pass 2: the run's rows, x * r_new.
+#pragma unroll
+        for (int j = 0; j < kKeep; ++j) {
+            if (j < n) {
+                float x[8];
+                widen_bf16x8(keep[j], x);
+                const int64_t row = static_cast<int64_t>(a.slots[t0 + j]) - page * block;
+                *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) = quantize8(x, r_new);
+            }
+        }
+        for (int j = kKeep; j < n; ++j) {
+            float x[8];
+            widen_bf16x8(*reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row), x);
+            const int64_t row = static_cast<int64_t>(a.slots[t0 + j]) - page * block;
+            *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) = quantize8(x, r_new);
+        }
+        if (lane == 0) *scale_slot = s_new;
+    }
+}
+
+constexpr int kGroup = 16;  // lanes per (member, head) in the generic kernel
+
+__global__ __launch_bounds__(kThreads) void append_fp8_generic(AppendArgs a) {
     const int64_t t = blockIdx.x;
     const int64_t pool = a.c.num_pages * a.c.block;
     const int64_t page = page_of(a.slots[t], a.c.block, pool);
@@ -64,36 +270,58 @@ __global__ __launch_bounds__(kThreads) void append_fp8(AppendArgs a) {
         for (int o = kGroup / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kGroup));
 
         float* scale_slot = a.c.scale + (page * 2 + m) * a.c.hkv + h;
-        const float s_old = fresh ? 0.0f : *scale_slot;
-        const float s_new = fmaxf(s_old, __fdiv_rn(amax, kFp8Max));
+        int k;
+        const float s_new = grow_scale(fresh ? 0.0f : *scale_slot, __fdiv_rn(amax, kFp8Max), k);
+        const float r_new = s_new > 0.0f ? __fdiv_rn(1.0f, s_new) : 0.0f;
         const int64_t head_base = page * a.c.s_page + m * a.c.s_kv + h * a.c.s_head;
 
-        if (!fresh && s_new > s_old && s_old > 0.0f) {
+        if (k > 0) {
             for (int64_t row = 0; row < a.c.block; ++row) {
                 if (written >> row & 1ull) continue;
                 uint8_t* p = cache + head_base + row * a.c.s_row;
-                for (int d = lane; d < a.c.d; d += kGroup) {
-                    const float x = __fdiv_rn(__fmul_rn(fp8_to_f32(p[d]), s_old), s_new);
-                    p[d] = f32_to_fp8(x);
-                }
+                for (int d = lane; d < a.c.d; d += kGroup)
+                    p[d] = f32_to_fp8(__builtin_amdgcn_ldexpf(fp8_to_f32(p[d]), -k));
             }
         }
         for (int64_t r = t; r < end; ++r) {
             uint8_t* p = cache + head_base + (a.slots[r] - page * a.c.block) * a.c.s_row;
             for (int d = lane; d < a.c.d; d += kGroup) {
                 const float x = load_as_f32(src, r * s_row + h * s_head + d, a.in_dt);
-                p[d] = s_new > 0.0f ? f32_to_fp8(__fdiv_rn(x, s_new)) : uint8_t{0};
+                p[d] = f32_to_fp8(__fmul_rn(x, r_new));
             }
         }
         if (lane == 0) *scale_slot = s_new;
     }
 }
 
+// Whether append_fp8_runs serves this append: bf16 rows of D 64, 128 or 256 whose 16-byte
+// chunks and 8-byte e4m3 chunks are aligned.
+bool runs_serve(const AppendArgs& a) {
+    const int d = a.c.d;
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    return a.in_dt == DT_BF16 && (d == 64 || d == 128 || d == 256) && a16(a.k) && a16(a.v) &&
+           a.k_srow % 8 == 0 && a.k_shead % 8 == 0 && a.v_srow % 8 == 0 && a.v_shead % 8 == 0 &&
+           (reinterpret_cast<uintptr_t>(a.c.base) & 7) == 0 && a.c.s_page % 8 == 0 &&
+           a.c.s_kv % 8 == 0 && a.c.s_row % 8 == 0 && a.c.s_head % 8 == 0;
+}
+
 }  // namespace
 
 hipError_t launch_append_fp8(const AppendArgs& a, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(append_fp8, dim3(static_cast<unsigned>(a.T)), dim3(kThreads), 0, s, a);
+    if (runs_serve(a)) {
+        // Rows per workgroup: one for decode-sized steps (every unit in parallel), growing with
+        // the step to a page's 16 rows (one page of every (member, head) per workgroup).
+        const int chunk = static_cast<int>(std::min<int64_t>(16, std::max<int64_t>(1, a.T / 2048)));
+        const dim3 grid(static_cast<unsigned>((a.T + chunk - 1) / chunk));
+        switch (a.c.d) {
+            case 64: hipLaunchKernelGGL(append_fp8_runs<64>, grid, dim3(kThreads), 0, s, a, chunk); break;
+            case 128: hipLaunchKernelGGL(append_fp8_runs<128>, grid, dim3(kThreads), 0, s, a, chunk); break;
+            default: hipLaunchKernelGGL(append_fp8_runs<256>, grid, dim3(kThreads), 0, s, a, chunk); break;
+        }
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(append_fp8_generic, dim3(static_cast<unsigned>(a.T)), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

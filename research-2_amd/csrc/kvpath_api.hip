@@ -90,23 +90,17 @@ int32_t check_rows(const kvpath_rows* x, const char* name, const char* what, int
     return KVPATH_OK;
 }
 
-int64_t n_parts_for(int64_t width, int64_t block, int32_t part) {
-    return (width * block + part - 1) / part;
-}
-
 struct WorkspaceLayout {
     int64_t o_bytes, ml_offset, total;
 };
 
-// The split-KV workspace: f32-sized partials [T, H, parts, D], then (m, l) [T, H, parts, 2].
-// total is -1 when a size overflows int64 (the caller refuses the call). Takes T, width and block
-// below 2^31 and H, D below 2^16.
-WorkspaceLayout workspace_layout(int64_t T, int64_t H, int64_t D, int64_t width, int64_t block,
-                                 int32_t part) {
-    const int64_t np = n_parts_for(width, block, part);
+// The split-KV workspace: f32-sized partials [T, H, slots, D], then (m, l) [T, H, slots, 2].
+// total is -1 when a size overflows int64 (the caller refuses the call). Takes T below 2^31 and
+// H, D below 2^16.
+WorkspaceLayout workspace_layout(int64_t T, int64_t H, int64_t D, int64_t slots) {
     WorkspaceLayout w{0, 0, -1};
     int64_t rows, o_vals, ml_vals;
-    if (__builtin_mul_overflow(T * H, np, &rows) || __builtin_mul_overflow(rows, D * 4, &o_vals) ||
+    if (__builtin_mul_overflow(T * H, slots, &rows) || __builtin_mul_overflow(rows, D * 4, &o_vals) ||
         __builtin_mul_overflow(rows, static_cast<int64_t>(8), &ml_vals) ||
         o_vals > (int64_t{1} << 62) || ml_vals > (int64_t{1} << 62))
         return w;
@@ -114,6 +108,22 @@ WorkspaceLayout workspace_layout(int64_t T, int64_t H, int64_t D, int64_t width,
     w.ml_offset = (w.o_bytes + 255) / 256 * 256;
     w.total = w.ml_offset + ml_vals;
     return w;
+}
+
+// The shape limits every attention entry point and size query shares: sizes below 2^31 (a
+// table spanning fewer than 2^31 keys), heads and head dims up to 2^16, a partition length that
+// is a multiple of 32 (0: the library's choice). Returns a message, or nullptr when the shape is
+// acceptable.
+const char* shape_problem(int64_t T, int64_t R, int64_t H, int64_t hkv, int64_t D, int64_t width,
+                          int64_t block, int32_t partition) {
+    if (T < 0 || R < 0 || H < 0 || hkv < 0 || D < 0 || width < 0 || block < 1)
+        return "negative or zero size";
+    if (T >= (1ll << 31) || R > 65535) return "plan too large";
+    if (H > kMaxHeads || hkv > kMaxHeads || D > kMaxDim) return "too many heads or head dims";
+    if (width >= (1ll << 31) || block >= (1ll << 31) || width * block >= (1ll << 31))
+        return "table spans too many keys";
+    if (partition < 0 || partition % 32 != 0) return "partition_tokens is not a multiple of 32";
+    return nullptr;
 }
 
 // Validates an append and fills its kernel arguments; launches nothing.
@@ -202,18 +212,19 @@ int32_t attend_args(const kvpath_rows* q, const kvpath::CacheView& c, const kvpa
     // Entries index the partition grid's z dimension (at most 65535).
     if (T > (1ll << 31) - 1 || R > 65535)
         return fail(KVPATH_EINVAL, "%s: plan too large", what);
-    const int32_t part = opts && opts->partition_tokens > 0
-                             ? opts->partition_tokens
-                             : kvpath::choose_partition(T, R, H, c.hkv, plan->table_width, c.block);
-    if (part % 32 != 0)
-        return fail(KVPATH_EINVAL, "%s: partition_tokens %d is not a multiple of 32", what, part);
-    // The grid's x dimension holds partitions x row-tile groups (at most 64).
-    if (plan->table_width >= (1ll << 31) || plan->table_width * c.block >= (1ll << 31) ||
-        n_parts_for(plan->table_width, c.block, part) * 64 >= (1ll << 31))
+    const int32_t req_part = opts ? opts->partition_tokens : 0;
+    if (req_part < 0 || req_part % 32 != 0)
+        return fail(KVPATH_EINVAL, "%s: partition_tokens %d is not a multiple of 32", what, req_part);
+    if (plan->table_width >= (1ll << 31) || plan->table_width * c.block >= (1ll << 31))
+        return fail(KVPATH_EINVAL, "%s: table spans too many keys", what);
+    const kvpath::SplitChoice split =
+        kvpath::choose_split(T, R, H, c.hkv, plan->table_width, c.block, req_part);
+    // The grid's x dimension holds partition slots x row-tile groups (at most 64).
+    if (static_cast<int64_t>(split.slots) * 64 >= (1ll << 31))
         return fail(KVPATH_EINVAL, "%s: table spans too many keys", what);
     if (opts && opts->window < 0)
         return fail(KVPATH_EINVAL, "%s: negative window %d", what, opts->window);
-    const WorkspaceLayout w = workspace_layout(T, H, c.d, plan->table_width, c.block, part);
+    const WorkspaceLayout w = workspace_layout(T, H, c.d, split.slots);
     if (w.total < 0) return fail(KVPATH_EINVAL, "%s: workspace size overflows", what);
     if (ws == nullptr || ws_bytes < w.total)
         return fail(KVPATH_EINVAL, "%s: workspace of %lld bytes, need %lld", what,
@@ -241,8 +252,10 @@ int32_t attend_args(const kvpath_rows* q, const kvpath::CacheView& c, const kvpa
     a.causal = opts ? (opts->causal != 0) : 1;
     a.sinks = opts ? opts->sinks : nullptr;
     a.score_scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(c.d)));
-    a.part = part;
-    a.n_parts = static_cast<int32_t>(n_parts_for(plan->table_width, c.block, part));
+    a.part = split.part;
+    a.part_fixed = split.fixed;
+    a.n_parts = split.slots;
+    a.grid_parts = kvpath::grid_slots(a.window, T, split.part, split.slots);
     a.tile_groups = 1;
     a.part_o = ws;
     // The partial format follows q alone, so kvpath_attend_partitions and kvpath_attend_reduce
@@ -266,7 +279,7 @@ int32_t attend_args(const kvpath_rows* q, const kvpath::CacheView& c, const kvpa
 
 extern "C" {
 
-int32_t kvpath_abi_version(void) { return 2; }
+int32_t kvpath_abi_version(void) { return 3; }
 
 const char* kvpath_last_error(void) { return g_error.c_str(); }
 
@@ -318,21 +331,34 @@ int32_t kvpath_copy_blocks(const kvpath_cache* cache, const int32_t* src, const 
                     "copy_blocks");
 }
 
-int32_t kvpath_partition_tokens(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
-                                int64_t kv_heads, int64_t table_width, int64_t block_size) {
-    return kvpath::choose_partition(num_tokens, num_reqs, num_heads, kv_heads, table_width,
-                                    block_size);
+int32_t kvpath_split_plan(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
+                          int64_t kv_heads, int64_t table_width, int64_t block_size,
+                          int32_t partition_tokens, kvpath_split* out) {
+    if (out == nullptr) return fail(KVPATH_EINVAL, "split_plan: null output");
+    if (const char* why = shape_problem(num_tokens, num_reqs, num_heads, kv_heads, 1, table_width,
+                                        block_size, partition_tokens))
+        return fail(KVPATH_EINVAL, "split_plan: %s", why);
+    if (kv_heads < 1 || num_heads % kv_heads != 0)
+        return fail(KVPATH_EINVAL, "split_plan: %lld q heads is not a multiple of %lld kv heads",
+                    (long long)num_heads, (long long)kv_heads);
+    const kvpath::SplitChoice sp = kvpath::choose_split(num_tokens, num_reqs, num_heads, kv_heads,
+                                                        table_width, block_size, partition_tokens);
+    out->partition_tokens = sp.part;
+    out->slots = sp.slots;
+    out->per_entry = sp.fixed ? 0 : 1;
+    return ok();
 }
 
-int64_t kvpath_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
-                               int64_t table_width, int64_t block_size, int32_t partition_tokens) {
-    // 0: the library's choice, which is never below 384 keys, so 384 bounds its workspace.
-    const int32_t part = partition_tokens > 0 ? partition_tokens : 384;
-    if (num_tokens < 0 || num_heads < 0 || head_dim < 0 || table_width < 0 || block_size < 1 ||
-        part % 32 != 0 || num_tokens >= (1ll << 31) || num_heads > kMaxHeads || head_dim > kMaxDim ||
-        table_width >= (1ll << 31) || block_size >= (1ll << 31) || table_width * block_size >= (1ll << 31))
+int64_t kvpath_workspace_bytes(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
+                               int64_t kv_heads, int64_t head_dim, int64_t table_width,
+                               int64_t block_size, int32_t partition_tokens) {
+    if (shape_problem(num_tokens, num_reqs, num_heads, kv_heads, head_dim, table_width, block_size,
+                      partition_tokens) != nullptr ||
+        kv_heads < 1 || num_heads % kv_heads != 0)
         return -1;
-    return workspace_layout(num_tokens, num_heads, head_dim, table_width, block_size, part).total;
+    const kvpath::SplitChoice sp = kvpath::choose_split(num_tokens, num_reqs, num_heads, kv_heads,
+                                                        table_width, block_size, partition_tokens);
+    return workspace_layout(num_tokens, num_heads, head_dim, sp.slots).total;
 }
 
 int32_t kvpath_attend(const kvpath_rows* q, const kvpath_cache* cache, const kvpath_plan* plan,

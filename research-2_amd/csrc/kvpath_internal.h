@@ -57,10 +57,13 @@ struct AttnArgs {
     int32_t window, causal;
     const float* sinks;
     float score_scale_log2;  // log2(e) / sqrt(D)
-    int32_t part;            // partition length in tokens (multiple of 32)
-    int32_t n_parts;         // partitions per entry: ceil(width*block / part)
-    int32_t grid_parts;      // partitions per entry in the grid: n_parts, or with a window only
-                             // as many as one entry's window can reach, from its first visible key
+    int32_t part;            // partition length in keys (multiple of 32): every entry's when
+                             // part_fixed, else the floor of each entry's own split
+    int32_t part_fixed;
+    int32_t n_parts;         // partition slots per entry (the workspace's partition dimension)
+    int32_t grid_parts;      // partition slots per entry in the grid: n_parts, or with a window
+                             // only as many as one entry's window can reach, from its first
+                             // visible key
     int32_t tile_groups;     // grid columns per partition (row tiles split across workgroups)
     // Partial outputs [T, H, n_parts, D]: with a bf16 q (part_bf16), each partition's output
     // normalized by its own sum and rounded to bf16 (the format vLLM's paged_attention_v2 and
@@ -94,9 +97,18 @@ bool attention_supported(const AttnArgs& a);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);  // partitions, then reduce
 // Whether the partition kernels can take this step's append in (k_new).
 bool attention_fuses(const AttnArgs& a);
-// The split-KV partition length (keys) the library picks for a step of this shape.
-int32_t choose_partition(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int64_t kv_heads,
-                         int64_t width, int64_t block);
+// How a step's keys are split into partitions: `part` keys each (fixed) or each entry's own
+// split with floor length `part` (split_entry, on the device), into at most `slots` per entry.
+struct SplitChoice {
+    int32_t part, slots, fixed;
+};
+// The split for a step of this shape; `partition` > 0 is a caller's fixed length.
+SplitChoice choose_split(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int64_t kv_heads,
+                         int64_t width, int64_t block, int32_t partition);
+// Partition slots per entry the grid holds (AttnArgs::grid_parts): all `slots`, or with a window
+// only as many as an entry's window reaches. The partition and reduce kernels both derive each
+// entry's split from it, so it is set once with the rest of the arguments.
+int32_t grid_slots(int32_t window, int64_t n_tokens, int32_t part, int32_t slots);
 hipError_t launch_partitions(const AttnArgs& a, hipStream_t s);
 hipError_t launch_reduce(const AttnArgs& a, hipStream_t s);
 

@@ -12,7 +12,6 @@ The op's signature, layout and plan contract are kelpie's `kelpie::paged_attenti
 """
 
 from kvpath.paged_attention import (
-    DEFAULT_PARTITION,
     KV_MEMBERS,
     assert_newest_positions,
     attend,
@@ -23,13 +22,12 @@ from kvpath.paged_attention import (
     no_sinks,
     paged_attention,
     paged_attention_fp8,
-    partition_tokens,
+    split_plan,
     workspace_bytes,
     write_kv,
 )
 
 __all__ = [
-    "DEFAULT_PARTITION",
     "KV_MEMBERS",
     "assert_newest_positions",
     "attend",
@@ -40,7 +38,7 @@ __all__ = [
     "no_sinks",
     "paged_attention",
     "paged_attention_fp8",
-    "partition_tokens",
+    "split_plan",
     "workspace_bytes",
     "write_kv",
 ]

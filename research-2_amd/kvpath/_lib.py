@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libkvpath.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, EINVAL, EUNSUPPORTED, ELAUNCH = 0, -1, -2, -3
 F32, F16, BF16, FP8_E4M3 = 0, 1, 2, 3
@@ -22,7 +22,7 @@ EXPORTS = (
     "kvpath_kv_append",
     "kvpath_kv_gather",
     "kvpath_copy_blocks",
-    "kvpath_partition_tokens",
+    "kvpath_split_plan",
     "kvpath_workspace_bytes",
     "kvpath_attend",
     "kvpath_attend_partitions",
@@ -82,6 +82,14 @@ class AttnOpts(ctypes.Structure):
     ]
 
 
+class Split(ctypes.Structure):
+    _fields_ = [
+        ("partition_tokens", ctypes.c_int32),
+        ("slots", ctypes.c_int32),
+        ("per_entry", ctypes.c_int32),
+    ]
+
+
 class KvpathError(RuntimeError):
     """A kvpath entry point returned an error status (argument contract or launch)."""
 
@@ -114,8 +122,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         "kvpath_kv_append": (i32, [p(Cache), p(Rows), p(Rows), p(Plan), vp]),
         "kvpath_kv_gather": (i32, [p(Cache), p(Plan), i64, vp, vp, vp]),
         "kvpath_copy_blocks": (i32, [p(Cache), vp, vp, i64, vp]),
-        "kvpath_partition_tokens": (i32, [i64, i64, i64, i64, i64, i64]),
-        "kvpath_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i32]),
+        "kvpath_split_plan": (i32, [i64, i64, i64, i64, i64, i64, i32, p(Split)]),
+        "kvpath_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64, i64, i32]),
         "kvpath_attend": (i32, [p(Rows), p(Cache), p(Plan), p(AttnOpts), p(Rows), vp, i64, vp]),
         "kvpath_attend_partitions": (i32, [p(Rows), p(Cache), p(Plan), p(AttnOpts), vp, i64, vp]),
         "kvpath_attend_reduce": (i32, [p(Rows), p(Cache), p(Plan), p(AttnOpts), p(Rows), vp, i64,

@@ -27,7 +27,6 @@ import torch
 from kvpath import _lib
 
 KV_MEMBERS = 2
-DEFAULT_PARTITION = 512
 # KVPATH_CHECK_POSITIONS=1: every op call also asserts on device that `positions` are the rows'
 # newest positions, as kelpie's op does (a device assert, no host sync, capture-safe). Off by
 # default: the kernels derive positions from seq_lens and never read `positions`.
@@ -153,9 +152,10 @@ def _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping, n_t
     return plan, tuple(keep)
 
 
-def _workspace(device: torch.device, n_tokens: int, n_heads: int, head_dim: int, width: int,
-               block: int, partition: int) -> torch.Tensor:
-    size = _lib.load().kvpath_workspace_bytes(n_tokens, n_heads, head_dim, width, block, partition)
+def _workspace(device: torch.device, n_tokens: int, n_reqs: int, n_heads: int, kv_heads: int,
+               head_dim: int, width: int, block: int, partition: int) -> torch.Tensor:
+    size = _lib.load().kvpath_workspace_bytes(n_tokens, n_reqs, n_heads, kv_heads, head_dim, width,
+                                              block, partition)
     if size < 0:
         raise ValueError("kvpath: bad workspace shape")
     ws = torch.empty(size + 256, dtype=torch.uint8, device=device)
@@ -190,18 +190,25 @@ def assert_newest_positions(row_request: torch.Tensor, positions: torch.Tensor,
     torch._assert_async(torch.all(ok | ~live), "plan rows are not their entry's newest positions")
 
 
-def partition_tokens(n_tokens: int, n_reqs: int, n_heads: int, kv_heads: int, width: int,
-                     block: int) -> int:
-    """The split-KV partition length the library picks for this step shape
-    (kvpath_partition_tokens): 512 keys for decode and verify, longer for prefill-sized steps."""
-    return _lib.load().kvpath_partition_tokens(n_tokens, n_reqs, n_heads, kv_heads, width, block)
+def split_plan(n_tokens: int, n_reqs: int, n_heads: int, kv_heads: int, width: int, block: int,
+               partition: int = 0) -> tuple[int, int, bool]:
+    """How the library splits a step of this shape into split-KV partitions (kvpath_split_plan):
+    (partition_tokens, slots, per_entry). With `partition` 0 each entry's keys are cut on the
+    device, from its own seq_len, into min(slots, ceil(span / partition_tokens)) equal partitions
+    rounded up to 32 keys; with `partition` > 0 every partition has that length."""
+    out = _lib.Split()
+    _lib.check("split_plan", _lib.load().kvpath_split_plan(n_tokens, n_reqs, n_heads, kv_heads,
+                                                           width, block, int(partition),
+                                                           ctypes.byref(out)))
+    return out.partition_tokens, out.slots, bool(out.per_entry)
 
 
-def workspace_bytes(n_tokens: int, n_heads: int, head_dim: int, width: int, block: int,
-                    partition: int = 0) -> int:
-    """Bytes of split-KV scratch one attention call of this shape needs (kvpath_workspace_bytes);
-    partition 0 sizes it for any partition length the library may choose."""
-    return _lib.load().kvpath_workspace_bytes(n_tokens, n_heads, head_dim, width, block, partition)
+def workspace_bytes(n_tokens: int, n_reqs: int, n_heads: int, kv_heads: int, head_dim: int,
+                    width: int, block: int, partition: int = 0) -> int:
+    """Bytes of split-KV scratch one attention call of this shape needs (kvpath_workspace_bytes)
+    at `partition` (0: the library's split)."""
+    return _lib.load().kvpath_workspace_bytes(n_tokens, n_reqs, n_heads, kv_heads, head_dim, width,
+                                              block, partition)
 
 
 # ---- entry points -------------------------------------------------------------------------------
@@ -240,14 +247,9 @@ def attend(q: torch.Tensor, kv_member: torch.Tensor, row_request: torch.Tensor,
     outr = _lib.Rows(out.data_ptr(), n_tokens, n_heads, head_dim, out.stride(0), head_dim,
                      _dtype_code(out, "out"))
     plan, keep = _plan(row_request, query_start_loc, seq_lens, block_table, None, n_tokens)
-    # Partition 0 goes down as 0 (the library's choice); the workspace is sized for the length
-    # the library picks.
-    part = int(partition) if partition > 0 else partition_tokens(
-        n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], block_table.shape[1],
-        kv_member.shape[2])
     opts, sinks = _opts(window, sinks, n_heads, causal, max(0, int(partition)))
-    ws = _workspace(dev, n_tokens, n_heads, head_dim, block_table.shape[1], kv_member.shape[2],
-                    part)
+    ws = _workspace(dev, n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], head_dim,
+                    block_table.shape[1], kv_member.shape[2], max(0, int(partition)))
     _lib.check("attend", lib.kvpath_attend(ctypes.byref(qr), ctypes.byref(cache),
                                            ctypes.byref(plan), ctypes.byref(opts),
                                            ctypes.byref(outr), ws.data_ptr(), ws.numel(),
@@ -274,12 +276,9 @@ def _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_star
                      _dtype_code(out, "out"))
     plan, keep = _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping,
                        n_tokens)
-    part = int(partition) if partition > 0 else partition_tokens(
-        n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], block_table.shape[1],
-        kv_member.shape[2])
     opts, sinks = _opts(window, sinks, n_heads, causal, max(0, int(partition)))
-    ws = _workspace(dev, n_tokens, n_heads, head_dim, block_table.shape[1], kv_member.shape[2],
-                    part)
+    ws = _workspace(dev, n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], head_dim,
+                    block_table.shape[1], kv_member.shape[2], max(0, int(partition)))
     _lib.check("paged_attention", lib.kvpath_paged_attention(
         ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), ctypes.byref(cache),
         ctypes.byref(plan), ctypes.byref(opts), ctypes.byref(outr), ws.data_ptr(), ws.numel(),
@@ -309,7 +308,8 @@ def paged_attention(  # noqa: PLR0913
     slot_mapping into `kv_member` (in place), then paged causal GQA attention -> [T, H * D] in
     q.dtype, pad rows exactly zero. Same 13 arguments, same order and meaning; the optional
     trailing `partition` (split-KV partition length in keys, 0 = the library's choice) is this
-    build's tuning knob and changes no result beyond fp32 rounding."""
+    build's tuning knob (a fixed split-KV partition length in keys; 0 = the library's split of
+    each entry by its own length) and changes no result beyond fp32 rounding."""
     return _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_start_loc,
                                  seq_lens, block_table, slot_mapping, window, sinks, causal, None,
                                  partition)

@@ -6,7 +6,7 @@ box has):
 
     python tests/golden/make_golden.py
 
-What it pins, that nothing else can: (1) that kvpath.samples.sample reproduces the reference's
+What it pins, that nothing else can: (1) that tests/reference_sample.py:sample reproduces the reference's
 sample() draw for draw (sha256 of every input tensor's bytes, per dtype), and (2) the reference's
 exact outputs -- fp64 (the truth), fp32 and bf16 -- and the bf16 pool after its write_kv, which
 the CPU oracle (oracle/attention.py) must reproduce. Reference: kelpie/kelpie-models/

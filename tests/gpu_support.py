@@ -5,7 +5,8 @@ from __future__ import annotations
 
 import torch
 
-from kvpath.samples import GARBAGE, KV_MEMBERS
+from kvpath.paged_attention import KV_MEMBERS
+from workloads import GARBAGE
 
 
 def compact_cpu(args: tuple, entries: list[int] | None = None, kv_scale=None) -> tuple:

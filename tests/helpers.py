@@ -6,7 +6,8 @@ import hashlib
 
 import torch
 
-from kvpath.samples import SAMPLE_BATCH, Batch
+from reference_sample import SAMPLE_BATCH
+from workloads import Batch
 
 
 def batch_of(meta_batch: dict) -> Batch:

@@ -205,8 +205,9 @@ int main() {
     plan.table_stride = kWidth;
     kvpath_attn_opts opts{};  // no window, no sinks, causal, the library's partition
     opts.causal = 1;
-    opts.partition_tokens = kvpath_partition_tokens(kRows, kEntries + 1, kHeads, kKvHeads, kWidth, kBlock);
-    const int64_t ws_bytes = kvpath_workspace_bytes(kRows, kHeads, kDim, kWidth, kBlock, opts.partition_tokens);
+    opts.partition_tokens = 0;
+    const int64_t ws_bytes =
+        kvpath_workspace_bytes(kRows, kEntries + 1, kHeads, kKvHeads, kDim, kWidth, kBlock, opts.partition_tokens);
     void *ws_g = nullptr, *ws_e = nullptr;
     CHECK_HIP(hipMalloc(&ws_g, ws_bytes));
     CHECK_HIP(hipMalloc(&ws_e, ws_bytes));

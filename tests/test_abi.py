@@ -50,14 +50,20 @@ def test_library_exports_every_symbol(lib) -> None:
 
 
 def test_workspace_bytes(lib) -> None:
-    # C2: T 64, H 32, D 128, table width 256 pages of 16 -> 8 partitions of 512
-    n = lib.kvpath_workspace_bytes(64, 32, 128, 256, 16, 512)
+    # C2 at a fixed 512-key partition: T 64, H 32, D 128, table width 256 pages of 16 -> 8 slots
+    n = lib.kvpath_workspace_bytes(64, 64, 32, 8, 128, 256, 16, 512)
     parts = 8
     o = 64 * 32 * parts * 128 * 4
     assert n == (o + 255) // 256 * 256 + 64 * 32 * parts * 2 * 4
-    assert lib.kvpath_workspace_bytes(64, 32, 128, 256, 16, 100) == -1  # not a multiple of 32
-    assert kvpath.workspace_bytes(4, 64, 128, 8192, 16) == lib.kvpath_workspace_bytes(
-        4, 64, 128, 8192, 16, 0)
+    assert lib.kvpath_workspace_bytes(64, 64, 32, 8, 128, 256, 16, 100) == -1  # not x 32
+    assert lib.kvpath_workspace_bytes(64, 64, 30, 8, 128, 256, 16, 0) == -1  # 30 q / 8 kv heads
+    assert kvpath.workspace_bytes(4, 4, 64, 8, 128, 8192, 16) == lib.kvpath_workspace_bytes(
+        4, 4, 64, 8, 128, 8192, 16, 0)
+    # The library's split: nine slots at config 2 however wide kelpie makes the table.
+    nine = 64 * 32 * 9
+    want = (nine * 128 * 4 + 255) // 256 * 256 + nine * 8
+    for width in (258, 512, 8192):
+        assert lib.kvpath_workspace_bytes(64, 64, 32, 8, 128, width, 16, 0) == want
 
 
 def _cache(**kw) -> _lib.Cache:
@@ -69,30 +75,33 @@ def _cache(**kw) -> _lib.Cache:
 
 
 @pytest.mark.parametrize("shape,want", [
-    ((64, 64, 32, 8, 258, 16), 512),        # decode (config 2)
-    ((64, 64, 32, 8, 256, 16), 480),        # 4096 keys: 9 partitions of 480, not 8 of 512
-    ((256, 16, 32, 8, 514, 16), 1024),      # verify, 16 rows per entry (config 3): 9 partitions
-    ((256, 16, 32, 8, 256, 16), 480),       # verify over 4096 keys: 1024 would leave 4 partitions
-    ((1024, 64, 32, 8, 514, 16), 1024),     # verify over 64 entries
-    ((4, 4, 64, 8, 8194, 16), 2048),        # 128k decode (config 5)
-    ((4, 4, 64, 8, 8192, 16), 1984),        # 131072 keys: 67 partitions, not 64
-    ((128, 128, 32, 8, 513, 16), 1024),     # fp8 decode over 2-8k keys (config 4)
-    ((2048, 4, 32, 8, 160, 16), 4096),      # prefill, 512-row chunks after 2k keys (config 6)
-    ((8192, 1, 32, 8, 2048, 16), 16352),    # one long prefill chunk: 1024+ workgroups, 3 parts
-    ((0, 0, 32, 8, 1, 16), 512),            # empty step
+    ((64, 64, 32, 8, 258, 16, 0), (512, 9, 1)),      # decode (config 2)
+    ((64, 64, 32, 8, 512, 16, 0), (512, 9, 1)),      # ... at kelpie's width for max_seq_len 8k
+    ((64, 64, 32, 8, 8192, 16, 0), (512, 9, 1)),     # ... and for 128k: the same grid
+    ((256, 16, 32, 8, 514, 16, 0), (896, 9, 1)),     # verify, 16 rows per entry (config 3)
+    ((256, 16, 32, 8, 8192, 16, 0), (896, 9, 1)),    # ... at kelpie's 128k width
+    ((1024, 64, 32, 8, 514, 16, 0), (896, 9, 1)),    # verify over 64 entries
+    ((4, 4, 64, 8, 8194, 16, 0), (512, 65, 1)),      # 128k decode (config 5): 2048+ workgroups
+    ((128, 128, 32, 8, 513, 16, 0), (512, 9, 1)),    # fp8 decode over 2-8k keys (config 4)
+    ((2048, 4, 32, 8, 160, 16, 0), (512, 1, 1)),     # prefill, 512-row chunks after 2k keys
+    ((8192, 1, 32, 8, 2048, 16, 0), (512, 3, 1)),    # one long prefill chunk: 1024 workgroups
+    ((64, 64, 32, 8, 3, 16, 0), (512, 1, 1)),        # a table of 48 keys: one slot
+    ((0, 0, 32, 8, 1, 16, 0), (512, 1, 1)),          # empty step
+    ((4, 4, 64, 8, 8192, 16, 512), (512, 256, 0)),   # a fixed 512: 256 partitions of 128k
+    ((64, 64, 32, 8, 258, 16, 480), (480, 9, 0)),    # a fixed 480 over 4128 keys
 ])
-def test_partition_choice(lib, shape, want) -> None:
-    """The library's split-KV choice: from 512 keys, longer while the table still splits into
-    8+ partitions over 2048+ workgroups (decode) or 1024+ (multi-row steps of one row group per
-    entry), or, once a step's rows give every partition eight or more workgroups (prefill),
-    while the grid keeps 1024+; then shortened by 32-key steps (to 3/4 at most) to an odd
-    partition count. The partition-0 workspace covers it."""
-    T, R, H, hkv, width, block = shape
-    part = lib.kvpath_partition_tokens(T, R, H, hkv, width, block)
-    assert part == want and part % 32 == 0 and part >= 384
-    assert kvpath.partition_tokens(*shape) == part
-    assert (lib.kvpath_workspace_bytes(T, H, 128, width, block, 0)
-            >= lib.kvpath_workspace_bytes(T, H, 128, width, block, part))
+def test_split_choice(lib, shape, want) -> None:
+    """The library's split-KV plan. With partition 0, each entry is cut on the device by its own
+    length: a floor of 512 keys (896 for verify-shaped steps), at most `slots` partitions per
+    entry, where the slots give the grid 2048+ workgroups (decode) or 1024+ (verify), at least
+    nine, an odd count, and never more than the table could fill at the floor; prefill-sized
+    steps fill the grid with rows and take slots only up to 1024 workgroups. A fixed partition
+    length gives ceil(keys / length) slots."""
+    T, R, H, hkv, width, block, part = shape
+    out = _lib.Split()
+    assert lib.kvpath_split_plan(T, R, H, hkv, width, block, part, ctypes.byref(out)) == _lib.OK
+    assert (out.partition_tokens, out.slots, out.per_entry) == want
+    assert kvpath.split_plan(T, R, H, hkv, width, block, part) == (want[0], want[1], bool(want[2]))
 
 
 def test_validation_refuses_before_any_launch(lib) -> None:
@@ -143,15 +152,16 @@ def test_oversized_shapes_are_refused(lib) -> None:
     """Sizes whose products would overflow int64, or that the kernels' int32 fields cannot
     hold, are refused on the host before any product is formed: workspace_bytes returns -1, the
     entry points EINVAL."""
-    assert lib.kvpath_workspace_bytes(1 << 31, 32, 128, 256, 16, 512) == -1
-    assert lib.kvpath_workspace_bytes(64, 1 << 20, 128, 256, 16, 512) == -1
-    assert lib.kvpath_workspace_bytes(64, 32, 1 << 20, 256, 16, 512) == -1
-    assert lib.kvpath_workspace_bytes(64, 32, 128, 1 << 40, 16, 512) == -1
-    assert lib.kvpath_workspace_bytes(64, 32, 128, 1 << 27, 1 << 8, 512) == -1
-    assert lib.kvpath_workspace_bytes((1 << 31) - 1, 1 << 16, 1 << 16, 4096, 16, 32) == -1
+    ws = lib.kvpath_workspace_bytes  # (T, R, H, Hkv, D, width, block, partition)
+    assert ws(1 << 31, 1, 32, 8, 128, 256, 16, 512) == -1
+    assert ws(64, 1 << 16, 32, 8, 128, 256, 16, 512) == -1
+    assert ws(64, 1, 1 << 20, 1, 128, 256, 16, 512) == -1
+    assert ws(64, 1, 32, 8, 1 << 20, 256, 16, 512) == -1
+    assert ws(64, 1, 32, 8, 128, 1 << 40, 16, 512) == -1
+    assert ws(64, 1, 32, 8, 128, 1 << 27, 1 << 8, 512) == -1
+    assert ws((1 << 31) - 1, 1, 1 << 16, 1 << 16, 1 << 16, 4096, 16, 32) == -1
     rows_parts = (1 << 20) * 64 * 8  # 256 x 16 keys in 512-key partitions
-    assert lib.kvpath_workspace_bytes(1 << 20, 64, 128, 256, 16, 512) == \
-        rows_parts * 128 * 4 + rows_parts * 8
+    assert ws(1 << 20, 1, 64, 8, 128, 256, 16, 512) == rows_parts * 128 * 4 + rows_parts * 8
 
     rows = _lib.Rows(0x2000, 4, 2, 64, 128, 64, _lib.BF16)
     plan = _lib.Plan(0x10, 0x20, 0x30, 0x40, 0x50, 4, 2, 3, 3)
@@ -189,7 +199,7 @@ def test_unsupported_is_not_implemented(lib) -> None:
     out = _lib.Rows(0x3000, 4, 4, 64, 256, 64, _lib.F32)
     plan = _lib.Plan(0x10, 0x20, 0x30, 0x40, 0x50, 4, 2, 3, 3)
     opts = _lib.AttnOpts(0, None, 1, 512)
-    ws = lib.kvpath_workspace_bytes(4, 4, 64, 3, 16, 512)
+    ws = lib.kvpath_workspace_bytes(4, 2, 4, 2, 64, 3, 16, 512)
     st = lib.kvpath_attend(ctypes.byref(q), ctypes.byref(cache), ctypes.byref(plan),
                            ctypes.byref(opts), ctypes.byref(out), 0x10000, ws, None)
     assert st == _lib.EUNSUPPORTED
@@ -199,7 +209,8 @@ def test_unsupported_is_not_implemented(lib) -> None:
 
 def test_python_layer_refuses_cpu_tensors() -> None:
     """There is no CPU path: CPU tensors raise instead of computing."""
-    from kvpath.samples import Batch, sample
+    from reference_sample import sample
+    from workloads import Batch
 
     args = sample(Batch(entries=((3, 1),), tokens=1, reqs=1, heads=4, kv_heads=2, head_dim=32,
                         block=4), "cpu", torch.bfloat16)
@@ -213,7 +224,8 @@ def test_newest_positions_assert() -> None:
     """kvpath.assert_newest_positions (the opt-in KVPATH_CHECK_POSITIONS check) accepts the
     sample plans and refuses a plan whose row sits at a wrong position, as kelpie's
     _assert_newest_positions does (on CPU tensors torch._assert_async raises at once)."""
-    from kvpath.samples import Batch, sample
+    from reference_sample import sample
+    from workloads import Batch
 
     batch = Batch(entries=((16, 1), (63, 4), (5, 16)), tokens=24, reqs=4, heads=8, kv_heads=2,
                   head_dim=32, block=16)
@@ -229,10 +241,13 @@ def test_newest_positions_assert() -> None:
     kvpath.assert_newest_positions(rr, pad, qsl, lens)
 
 
-def test_partition_choice_properties(lib) -> None:
-    """Over a seeded sweep of step shapes: the chosen partition is a multiple of 32 and at least
-    384 keys, and the partition-0 workspace covers the workspace of the choice."""
+def test_split_choice_properties(lib) -> None:
+    """Over a seeded sweep of step shapes: the floor length is a multiple of 32 of at least 512
+    keys; the slots are at least one, no more than the table could fill at the floor, and do not
+    grow with the table's width once it exceeds that (kelpie pads tables to max_seq_len); the
+    workspace is exactly the slots' partials."""
     g = torch.Generator().manual_seed(5)
+    out = _lib.Split()
     for _ in range(400):
         T = int(torch.randint(1, 9000, (1,), generator=g))
         R = int(torch.randint(1, min(T, 512) + 1, (1,), generator=g))
@@ -240,8 +255,14 @@ def test_partition_choice_properties(lib) -> None:
         H = hkv * [1, 2, 4, 8][int(torch.randint(4, (1,), generator=g))]
         block = [16, 32, 64][int(torch.randint(3, (1,), generator=g))]
         width = int(torch.randint(1, 9000, (1,), generator=g))
-        part = lib.kvpath_partition_tokens(T, R, H, hkv, width, block)
-        assert part % 32 == 0 and part >= 384, (T, R, H, hkv, width, block, part)
+        shape = (T, R, H, hkv, width, block)
+        assert lib.kvpath_split_plan(*shape, 0, ctypes.byref(out)) == _lib.OK
+        part, slots = out.partition_tokens, out.slots
+        assert out.per_entry == 1 and part % 32 == 0 and part >= 512, shape
+        assert 1 <= slots <= max(1, -(-width * block // part)), shape
+        assert lib.kvpath_split_plan(T, R, H, hkv, width * 64, block, 0, ctypes.byref(out)) == 0
+        assert out.slots >= slots and (slots == -(-width * block // part) or out.slots == slots)
         for dim in (64, 128):
-            assert (lib.kvpath_workspace_bytes(T, H, dim, width, block, 0)
-                    >= lib.kvpath_workspace_bytes(T, H, dim, width, block, part))
+            rows = T * H * slots
+            want = (rows * dim * 4 + 255) // 256 * 256 + rows * 8
+            assert lib.kvpath_workspace_bytes(T, R, H, hkv, dim, width, block, 0) == want, shape

@@ -9,7 +9,7 @@ import subprocess
 import sys
 
 import bench
-from kvpath.samples import Batch
+from workloads import Batch
 
 
 def _decode(lens, heads=32, kv_heads=8, dim=128, window=0):
@@ -75,3 +75,31 @@ def test_verify_rows_are_causal() -> None:
     b = bench.step_bytes(batch, partition=512)
     assert b["kv"] == 100 * 2 * 8 * 128 * 2
     assert b["flops"] == sum(32 * (84 + i + 1) * 4 * 128 for i in range(16))
+
+
+def test_per_entry_split_covers_each_entry() -> None:
+    """The library's per-entry split (mirrored in bench.entry_split): partitions of a multiple of
+    32 keys, at most `slots` of them, at most the floor length while the slots suffice, covering
+    [anchor, n) with no partition left empty; a window anchors at the first visible key's
+    32-key block."""
+    for n in (1, 31, 32, 33, 511, 512, 513, 1500, 4096, 4097, 8208, 131072):
+        for slots in (1, 3, 9, 65):
+            anchor, part = bench.entry_split(n, 1, 0, 512, slots)
+            count = -(-(n - anchor) // part)
+            assert anchor == 0 and part % 32 == 0 and 1 <= count <= slots, (n, slots, part)
+            if -(-n // 512) <= slots:
+                assert part <= 512 and count == -(-n // 512), (n, slots, part)
+            assert (count - 1) * part < n - anchor <= count * part
+    anchor, part = bench.entry_split(1000, 1, 128, 512, 9, 1)
+    assert anchor == (1000 - 1 - 128 + 1) // 32 * 32 and part >= 1000 - anchor
+    assert bench.entry_split(1000, 1, 0, 384, None) == (0, 384)
+
+
+def test_split_bytes_count_partitions_per_entry() -> None:
+    """With the per-entry split, each decode row writes one partial per partition of its own
+    entry: ceil(n / 512) while that fits the slots, else `slots`."""
+    lens = [100, 1500, 4096, 6000]
+    b = bench.step_bytes(_decode(lens), partition=512, slots=9)
+    counts = [min(9, -(-n // 512)) for n in lens]
+    parts = sum(32 * c for c in counts) * (128 * 2 + 8)
+    assert b["reduce"] == parts + len(lens) * 32 * 128 * 2

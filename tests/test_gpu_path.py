@@ -16,7 +16,8 @@ import torch
 import kvpath
 from gpu_support import compact_cpu, dequantized
 from helpers import digest, golden_batch, within
-from kvpath.samples import Batch, config_batch, copy_pairs, sample, synthetic
+from reference_sample import sample
+from workloads import Batch, config_batch, copy_pairs, synthetic
 from oracle import attention as oracle
 from oracle import kvbytes
 
@@ -180,11 +181,14 @@ def test_copy_blocks_bit_exact(dtype, heads, dim, block) -> None:
 # ---- fp8 quantize-on-append: bytes and scales bit-exact ---------------------------------------------
 
 
-def test_fp8_append_bit_exact_over_steps() -> None:
+@pytest.mark.parametrize("dim,in_dtype", [(128, torch.bfloat16), (64, torch.bfloat16),
+                                          (256, torch.bfloat16), (128, torch.float32)])
+def test_fp8_append_bit_exact_over_steps(dim, in_dtype) -> None:
     """A prefill chunk, then decode steps and a multi-row step, into an fp8 member with stale
-    scales and bytes: every page's bytes and scales equal the C oracle's after each step."""
-    say("fp8 append steps")
-    pages, block, heads, dim = 40, 16, 8, 128
+    scales and bytes: every page's bytes and scales equal the C oracle's after each step (bf16
+    rows at D 64/128/256 take the run kernel, f32 rows the generic one)."""
+    say("fp8 append steps", dim, in_dtype)
+    pages, block, heads = 40, 16, 8
     kv = _engine_member(pages, block, heads, dim, torch.uint8).view(torch.float8_e4m3fn)
     g = torch.Generator().manual_seed(7)
     kv.view(torch.uint8).copy_(torch.randint(0, 120, kv.shape, generator=g, dtype=torch.uint8).cuda())
@@ -205,8 +209,8 @@ def test_fp8_append_bit_exact_over_steps() -> None:
         t = len(slots)
         x = torch.randn(t, heads, dim, generator=g)
         x = torch.where(torch.rand(t, heads, dim, generator=g) < 0.01, x * 20, x)
-        k = x.to(torch.bfloat16)
-        v = (torch.randn(t, heads, dim, generator=g) * (1 + lens[0] % 3)).to(torch.bfloat16)
+        k = x.to(torch.bfloat16).to(in_dtype)
+        v = (torch.randn(t, heads, dim, generator=g) * (1 + lens[0] % 3)).to(in_dtype)
         s = torch.tensor(slots, dtype=torch.int32)
         kvbytes.kv_append_fp8(ref_kv, ref_scale, k, v, s)
         kvpath.write_kv(kv, k.cuda(), v.cuda(), s.cuda(), scale)
@@ -216,9 +220,39 @@ def test_fp8_append_bit_exact_over_steps() -> None:
         assert torch.equal(scale.cpu()[1:], ref_scale[1:]), rows
 
     step([37, 5, 16])     # prefill: fresh pages, partial and full
-    for _ in range(6):
+    for _ in range(12):
         step([1, 1, 1])   # decode: scale growth + requantization
     step([4, 0, 20])      # multi-row step across a page boundary
+
+
+@pytest.mark.parametrize("offset", [0, 5])
+def test_fp8_append_prefill_sized_bit_exact(offset) -> None:
+    """Prefill-sized fp8 appends (34,000 rows: the run kernel's 16-row chunks) starting at a page
+    boundary or mid-page (runs then straddle the chunks), with stale bytes and scales, and a
+    last row whose slot lies outside the pool: bytes and scales equal the C oracle's. (A step's
+    rows that share a page are consecutive, as in every kelpie plan.)"""
+    say("fp8 append prefill-sized, offset", offset)
+    pages, block, heads, dim = 2400, 16, 8, 128
+    kv = _engine_member(pages, block, heads, dim, torch.uint8).view(torch.float8_e4m3fn)
+    g = torch.Generator().manual_seed(11 + offset)
+    kv.view(torch.uint8).copy_(torch.randint(0, 120, kv.shape, generator=g, dtype=torch.uint8).cuda())
+    scale = (torch.rand(pages, 2, heads, generator=g) * 0.05).cuda()
+    ref_kv = compact_member(kv)
+    ref_scale = scale.cpu().clone()
+    rows = 34000
+    order = (torch.randperm(pages - 1, generator=g) + 1)
+    pos = torch.arange(offset, offset + rows)
+    slots = (order[pos // block] * block + pos % block).to(torch.int32)
+    slots[-1] = pages * block + 7  # outside the pool (last, as pad rows come): skipped
+    x = torch.randn(rows, heads, dim, generator=g)
+    k = torch.where(torch.rand(rows, heads, dim, generator=g) < 0.01, x * 20, x).to(torch.bfloat16)
+    v = torch.randn(rows, heads, dim, generator=g).to(torch.bfloat16)
+    kvbytes.kv_append_fp8(ref_kv, ref_scale, k, v, slots)
+    kvpath.write_kv(kv, k.cuda(), v.cuda(), slots.cuda(), scale)
+    torch.cuda.synchronize()
+    assert torch.equal(compact_member(kv)[1:].contiguous().view(torch.uint8),
+                       ref_kv[1:].contiguous().view(torch.uint8))
+    assert torch.equal(scale.cpu()[1:], ref_scale[1:])
 
 
 # ---- attention: golden cases and the configurations ---------------------------------------------------
@@ -486,16 +520,15 @@ def test_split_entry_points_match_attend(cfg) -> None:
     q, k, v, kv_member, rr, pos, qsl, lens, table, slots, window, sinks, causal = sample(
         batch, "cuda", torch.bfloat16, seed=40 + cfg)
     kvpath.write_kv(kv_member, k, v, slots)
-    part = kvpath.partition_tokens(q.shape[0], lens.shape[0], q.shape[1], kv_member.shape[3],
-                                   table.shape[1], kv_member.shape[2])
+    part = 0  # the library's split of each entry by its own length
     want = kvpath.attend(q, kv_member, rr, qsl, lens, table, window, sinks, causal, partition=part)
     lib = _lib.load()
     cache = _cache(kv_member, None)
     qr, qq = _rows(q, "q")
     plan, keep = _plan(rr, qsl, lens, table, None, q.shape[0])
     opts, sinks32 = _opts(window, sinks, q.shape[1], causal, part)
-    ws = _workspace(q.device, q.shape[0], q.shape[1], q.shape[2], table.shape[1],
-                    kv_member.shape[2], part)
+    ws = _workspace(q.device, q.shape[0], lens.shape[0], q.shape[1], kv_member.shape[3],
+                    q.shape[2], table.shape[1], kv_member.shape[2], part)
     got = torch.full_like(want, float("nan"))
     outr = _lib.Rows(got.data_ptr(), q.shape[0], q.shape[1], q.shape[2], got.stride(0),
                      q.shape[2], _dtype_code(got, "out"))

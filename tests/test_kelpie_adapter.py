@@ -84,7 +84,8 @@ def test_impl_refuses_cpu_like_the_op(fake_kelpie) -> None:
     import torch
 
     from kvpath import kelpie_adapter
-    from kvpath.samples import Batch, sample
+    from reference_sample import sample
+    from workloads import Batch
 
     args = sample(Batch(entries=((3, 1),), tokens=1, reqs=1, heads=4, kv_heads=2, head_dim=32,
                         block=4), "cpu", torch.bfloat16)

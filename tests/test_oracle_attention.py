@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from helpers import digest, golden_batch
-from kvpath.samples import Batch, sample
+from reference_sample import sample
+from workloads import Batch
 from oracle import attention as oracle
 
 
@@ -29,7 +30,7 @@ def _outs(arrays: dict, name: str) -> dict[str, torch.Tensor]:
 
 
 def test_sample_reproduces_reference_draws(golden) -> None:
-    """kvpath.samples.sample == the reference's sample() byte for byte, every case and dtype."""
+    """reference_sample.sample == the reference's sample() byte for byte, every case and dtype."""
     meta, _ = golden
     for name, entry in meta.items():
         batch = golden_batch(name, meta)

@@ -13,7 +13,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kvpath.samples import Batch, sample
+from reference_sample import sample
+from workloads import Batch
 from oracle import attention as oracle_attn
 from oracle import kvbytes
 
@@ -160,7 +161,7 @@ def _bf16(*shape, g, outliers=0.0):
 
 def test_fp8_fresh_page_closed_form() -> None:
     """A step writing rows 0..3 of a page: scale = absmax/448 per (member, head), bytes = torch's
-    e4m3 cast of clamp(x / scale)."""
+    e4m3 cast of clamp(x * (1 / scale))."""
     g = torch.Generator().manual_seed(4)
     kv, scale = _fp8_member()
     k, v = _bf16(4, 2, 16, g=g), _bf16(4, 2, 16, g=g)
@@ -171,13 +172,22 @@ def test_fp8_fresh_page_closed_form() -> None:
             xf = x[:, h].float()
             s = xf.abs().max() / 448.0
             assert scale[2, m, h] == s
-            want = (xf / s).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+            want = (xf * (1.0 / s)).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
             assert torch.equal(kv[2, m, :4, h].view(torch.uint8), want)
 
 
+def _growth(s_old: torch.Tensor, t: torch.Tensor) -> int:
+    """The smallest k >= 1 with s_old * 2^k >= t, by exact power-of-two products."""
+    k = 1
+    while bool(torch.ldexp(s_old, torch.tensor(k)) < t):
+        k += 1
+    return k
+
+
 def test_fp8_requantizes_on_scale_growth() -> None:
-    """Rows 0..3, then row 4 with a larger absmax: rows 0..3 become e4m3(f32(q) * s_old / s_new),
-    row 4 e4m3(x / s_new); a later smaller row keeps the scale."""
+    """Rows 0..3, then row 4 with a larger absmax: the scale grows by the smallest power of two
+    2^k that covers absmax/448, rows 0..3 become e4m3(clamp(f32(q) * 2^-k)) and row 4
+    e4m3(clamp(x * (1 / s_new))); a later smaller row keeps the scale."""
     g = torch.Generator().manual_seed(5)
     kv, scale = _fp8_member()
     k1, v1 = _bf16(4, 2, 16, g=g), _bf16(4, 2, 16, g=g)
@@ -185,20 +195,55 @@ def test_fp8_requantizes_on_scale_growth() -> None:
     old_bytes, old_scale = kv[1].clone(), scale[1].clone()
     k2, v2 = (_bf16(1, 2, 16, g=g).float() * 8).to(torch.bfloat16), _bf16(1, 2, 16, g=g)
     kvbytes.kv_append_fp8(kv, scale, k2, v2, torch.tensor([20], dtype=torch.int32))
+    grew = 0
     for m, x in enumerate((k2, v2)):
         for h in range(2):
             s_old = old_scale[m, h]
-            s_new = torch.maximum(s_old, x[0, h].float().abs().max() / 448.0)
+            t = x[0, h].float().abs().max() / 448.0
+            k = _growth(s_old, t) if t > s_old else 0
+            s_new = torch.ldexp(s_old, torch.tensor(k))
             assert scale[1, m, h] == s_new
             old = old_bytes[m, :4, h].float()
-            if s_new > s_old:
-                want = ((old * s_old) / s_new).clamp(-448, 448).to(torch.float8_e4m3fn)
+            if k:
+                grew += 1
+                want = torch.ldexp(old, torch.tensor(-k)).clamp(-448, 448).to(torch.float8_e4m3fn)
             else:
                 want = old_bytes[m, :4, h]
             assert torch.equal(kv[1, m, :4, h].view(torch.uint8), want.view(torch.uint8))
-            new = (x[0, h].float() / s_new).clamp(-448, 448).to(torch.float8_e4m3fn)
+            new = (x[0, h].float() * (1.0 / s_new)).clamp(-448, 448).to(torch.float8_e4m3fn)
             assert torch.equal(kv[1, m, 4, h].view(torch.uint8), new.view(torch.uint8))
-    assert bool((scale[1, 0] > old_scale[0]).all())  # K grew (x8); the rule fired
+    assert grew >= 2 and bool((scale[1, 0] > old_scale[0]).all())  # K grew (x8); the rule fired
+
+
+def test_fp8_growth_keeps_dequantized_values() -> None:
+    """A scale growth is an exponent shift: every requantized element whose value stays an e4m3
+    normal dequantizes to exactly what it did before (no rounding compounds over a decode
+    stream); a fresh page's largest element maps to 448 and comes back to within the f32
+    rounding of its scale."""
+    g = torch.Generator().manual_seed(9)
+    kv, scale = _fp8_member(pages=3)
+    before_vals = None
+    for row in range(16):
+        k = (_bf16(1, 2, 16, g=g).float() * (1.0 + row / 3)).to(torch.bfloat16)
+        v = _bf16(1, 2, 16, g=g)
+        if row == 0:
+            kvbytes.kv_append_fp8(kv, scale, k, v, torch.tensor([16], dtype=torch.int32))
+            first = k[0].float().abs().amax(dim=-1)
+            deq0 = kvbytes.e4m3_decode(kv[1, 0, 0].contiguous()).reshape(2, 16) * scale[1, 0][:, None]
+            torch.testing.assert_close(deq0.abs().amax(dim=-1), first, rtol=2.0 ** -23, atol=0)
+        else:
+            kvbytes.kv_append_fp8(kv, scale, k, v, torch.tensor([16 + row], dtype=torch.int32))
+        q = kv[1, 0, :row].contiguous()
+        vals = kvbytes.e4m3_decode(q).reshape(row, 2, 16) * scale[1, 0][None, :, None]
+        if before_vals is not None and row > 1:
+            prev = before_vals[:row - 1]
+            now = vals[:row - 1]
+            # elements that are e4m3 normals after the shift (|q| >= 2^-6) keep their value
+            normal = kvbytes.e4m3_decode(q[:row - 1]).reshape(row - 1, 2, 16).abs() >= 2.0 ** -6
+            assert torch.equal(now[normal], prev[normal]), row
+        before_vals = kvbytes.e4m3_decode(kv[1, 0, :row + 1].contiguous()).reshape(row + 1, 2, 16) \
+            * scale[1, 0][None, :, None]
+    assert bool((scale[1, 0] > 0).all())
 
 
 def test_fp8_step_order_independent_and_monotone() -> None:

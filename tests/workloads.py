@@ -1,14 +1,15 @@
-"""Seeded inputs for the op, laid out as kelpie's engine lays them out.
+"""Seeded step workloads for the tests and the bench, laid out as kelpie's engine lays them out.
 
-`Batch` and `sample` mirror the op's own sample generator (kelpie/kelpie-models/kelpie_models/
-kernels/ops/paged_attention.py:270-369) draw for draw, so `sample(batch, device, dtype, seed)`
-returns the same tensors the reference's does: K/V interleaved per row of a two-member page
-(`kv_member` is a strided view, like the arena's), pages handed out in a random order, page 0
-the null page, the scratch slot its last row, GARBAGE in never-written slots, values drawn in fp32
-and rounded to bf16 so a float64 sample is the bf16 sample's exact truth.
-
-`synthetic` builds the same structure at pool scale (tens of thousands of pages, millions of
-context rows) directly on the device, for the BASELINE configurations; `config` names them.
+`Batch` describes one layer's step as the reference's generator does (kelpie/kelpie-models/
+kelpie_models/kernels/ops/paged_attention.py:270-293). `synthetic` builds it at pool scale (tens of
+thousands of pages, millions of context rows) directly on the device: this layer is member m of
+an arena of `members` layers (K/V interleaved per row, sdk/kv.py:163-224), pages handed out in a
+random order, page 0 the null page, the scratch slot its last row, GARBAGE in never-written
+slots, values N(0,1) rounded to bf16. Block tables are as wide as the batch needs, or as wide as
+kelpie-core makes them for a `max_seq_len` (scheduler.zig:1577-1578: max_blocks_per_req =
+ceil(max_seq_len / block), null pages past each request's own, c_api.zig:1149-1150).
+`config_batch` names BASELINE.json's configurations 1-5 and workloads 6-9. Test and bench input
+only: the library never imports this module.
 """
 
 from __future__ import annotations
@@ -46,75 +47,6 @@ class Batch:
         return sum(rows for _, rows in self.entries)
 
 
-def sample(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed: int = 0) -> tuple:
-    """The op's 13 arguments for `batch` (ops/paged_attention.py:300-367, same draw order)."""
-    g = torch.Generator(device="cpu").manual_seed(seed)
-    b = batch
-    assert b.n_rows <= b.tokens and len(b.entries) <= b.reqs, b
-    assert b.heads % b.kv_heads == 0, b
-
-    def draw(*shape: int) -> torch.Tensor:
-        return torch.randn(*shape, generator=g).to(torch.bfloat16).to(device=device, dtype=dtype)
-
-    lens = [ctx + rows for ctx, rows in b.entries]
-    need = [-(-n // b.block) for n in lens]
-    width = max(need, default=1) + b.spare_pages
-    n_pages = 1 + sum(need)
-    order = (torch.randperm(n_pages - 1, generator=g) + 1).tolist()
-    table = torch.zeros(b.reqs, width, dtype=torch.int32)
-    for r, n in enumerate(need):
-        table[r, :n] = torch.tensor(order[:n], dtype=torch.int32)
-        order = order[n:]
-    arena = torch.full((n_pages, b.block, 2, KV_MEMBERS, b.kv_heads, b.head_dim), GARBAGE,
-                       dtype=dtype, device=device)
-    kv_member = arena[:, :, 1].permute(0, 2, 1, 3, 4)
-    flat_k, flat_v = kv_views(kv_member)
-    flat_k[: b.block].copy_(draw(b.block, b.kv_heads, b.head_dim))
-    flat_v[: b.block].copy_(draw(b.block, b.kv_heads, b.head_dim))
-
-    row_request = torch.full((b.tokens,), -1, dtype=torch.int32)
-    positions = torch.zeros(b.tokens, dtype=torch.int32)
-    slot_mapping = torch.full((b.tokens,), b.block - 1, dtype=torch.int32)
-    seq_lens = torch.ones(b.reqs, dtype=torch.int32)
-    query_start_loc = torch.full((b.reqs + 1,), b.n_rows, dtype=torch.int32)
-    query_start_loc[0] = 0
-    row = 0
-    for r, (ctx, rows) in enumerate(b.entries):
-        pos = torch.arange(ctx + rows)
-        slots = table[r, pos // b.block] * b.block + (pos % b.block).to(torch.int32)
-        flat_k.index_copy_(0, slots[:ctx].to(device).long(), draw(ctx, b.kv_heads, b.head_dim))
-        flat_v.index_copy_(0, slots[:ctx].to(device).long(), draw(ctx, b.kv_heads, b.head_dim))
-        row_request[row: row + rows] = r
-        positions[row: row + rows] = torch.arange(ctx, ctx + rows, dtype=torch.int32)
-        slot_mapping[row: row + rows] = slots[ctx:]
-        seq_lens[r] = ctx + rows
-        row += rows
-        query_start_loc[r + 1] = row
-    sinks = (torch.randn(b.heads, generator=g) * 2).to(device) if b.sinks else no_sinks(
-        torch.empty(0, device=device))
-    return (
-        draw(b.tokens, b.heads, b.head_dim),
-        draw(b.tokens, b.kv_heads, b.head_dim),
-        draw(b.tokens, b.kv_heads, b.head_dim),
-        kv_member,
-        row_request.to(device),
-        positions.to(device),
-        query_start_loc.to(device),
-        seq_lens.to(device),
-        table.to(device),
-        slot_mapping.to(device),
-        b.window,
-        sinks,
-        b.causal,
-    )
-
-
-# A small odd case, the reference's own (ops/paged_attention.py:370-373): GQA 2, one entry with
-# context + two rows, one decode row, a pad entry and a pad row, window 3, sinks.
-SAMPLE_BATCH = Batch(entries=((5, 2), (3, 1)), tokens=4, reqs=3, heads=4, kv_heads=2,
-                     head_dim=32, block=4, window=3)
-
-
 # ---- pool-scale inputs ---------------------------------------------------------------------------
 
 
@@ -127,6 +59,7 @@ class Step:
     batch: Batch
     pool_pages: int
     free_pages: torch.Tensor  # int32 page ids no entry uses (copy_blocks destinations)
+    arena: torch.Tensor | None = None  # the whole arena the member views
     extra: dict = field(default_factory=dict)
 
     @property
@@ -134,13 +67,38 @@ class Step:
         return self.args[3]
 
 
+def new_arena(batch: Batch, pool_pages: int, device: str | torch.device, cache_dtype,
+              members: int = 2) -> torch.Tensor:
+    """An arena of `members` layers over `pool_pages` pages, [pages, block, members, 2, Hkv, D]
+    (K/V interleaved per row, every layer's row together, as sdk/kv.py:163-224 lays a group's
+    unit out): GARBAGE everywhere, zero bytes for an fp8 cache."""
+    b = batch
+    shape = (pool_pages, b.block, members, KV_MEMBERS, b.kv_heads, b.head_dim)
+    if cache_dtype == torch.float8_e4m3fn:
+        return torch.zeros(shape, dtype=torch.uint8, device=device).view(torch.float8_e4m3fn)
+    return torch.full(shape, GARBAGE, dtype=cache_dtype, device=device)
+
+
+def table_width(batch: Batch, max_seq_len: int = 0) -> int:
+    """Block-table columns: the batch's widest entry plus spare pages, or kelpie-core's
+    max_blocks_per_req = ceil(max_seq_len / block) when `max_seq_len` is given."""
+    need = max((-(-(ctx + rows) // batch.block) for ctx, rows in batch.entries), default=1)
+    if max_seq_len > 0:
+        width = -(-max_seq_len // batch.block)
+        assert need <= width, (need, width)
+        return width
+    return need + batch.spare_pages
+
+
 def synthetic(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed: int = 0, *,
               pool_pages: int | None = None, outliers: float = 0.0, cache_dtype=None,
-              members: int = 2, chunk_rows: int = 1 << 18) -> Step:
-    """`batch` at pool scale, built on the device. Same layout rules as `sample` (this layer is
-    member 1 of `members`, random page order, null page 0, scratch slot its last row, GARBAGE
-    in unwritten slots; values N(0,1) rounded to bf16), but pages are drawn from a pool of
-    `pool_pages` (the rest stay free) and the values come from a device generator.
+              members: int = 2, member: int | None = None, arena: torch.Tensor | None = None,
+              max_seq_len: int = 0, chunk_rows: int = 1 << 18) -> Step:
+    """`batch` at pool scale, built on the device: this layer is member `member` (default the
+    last) of an arena of `members` layers, either a fresh one or `arena` (new_arena) shared with
+    other steps, pages drawn at random from its `pool_pages` (the rest stay free), values from a
+    device generator. `max_seq_len` > 0 pads every block-table row with null pages to kelpie's
+    width for that maximum.
 
     `outliers` > 0 multiplies that fraction of K/V context elements (and of the step's k/v) by
     20. `cache_dtype=torch.float8_e4m3fn` stores the context through kvpath's quantize-on-append
@@ -152,9 +110,15 @@ def synthetic(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed
     gd = torch.Generator(device=device).manual_seed(seed + 1)
     lens = [ctx + rows for ctx, rows in b.entries]
     need = [-(-n // b.block) for n in lens]
-    width = max(need, default=1) + b.spare_pages
+    width = table_width(b, max_seq_len)
     used = sum(need)
-    pool = max(pool_pages or 0, used + 1)
+    if arena is not None:
+        pool, members = arena.shape[0], arena.shape[2]
+        assert pool >= used + 1, (pool, used)
+    else:
+        pool = max(pool_pages or 0, used + 1)
+        arena = new_arena(b, pool, device, cache_dtype, members)
+    member = members - 1 if member is None else member
     perm = (torch.randperm(pool - 1, generator=gc) + 1).to(torch.int32)
     table = torch.zeros(b.reqs, width, dtype=torch.int32)
     at = 0
@@ -163,13 +127,7 @@ def synthetic(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed
         at += n
     free_pages = perm[at:].clone()
 
-    if cache_dtype == torch.float8_e4m3fn:
-        arena = torch.zeros((pool, b.block, members, KV_MEMBERS, b.kv_heads, b.head_dim),
-                            dtype=torch.uint8, device=device).view(torch.float8_e4m3fn)
-    else:
-        arena = torch.full((pool, b.block, members, KV_MEMBERS, b.kv_heads, b.head_dim),
-                           GARBAGE, dtype=cache_dtype, device=device)
-    kv_member = arena[:, :, members - 1].permute(0, 2, 1, 3, 4)
+    kv_member = arena[:, :, member].permute(0, 2, 1, 3, 4)
     kv_scale = new_kv_scale(kv_member) if cache_dtype == torch.float8_e4m3fn else None
 
     def draw(n: int, heads: int) -> torch.Tensor:
@@ -218,7 +176,7 @@ def synthetic(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed
     args = (q, k, v, kv_member, row_request.to(device), positions.to(device),
             query_start_loc.to(device), seq_lens.to(device), table_dev, slot_mapping.to(device),
             b.window, sinks, b.causal)
-    return Step(args, kv_scale, b, pool, free_pages.to(device))
+    return Step(args, kv_scale, b, pool, free_pages.to(device), arena)
 
 
 # ---- the BASELINE configurations -----------------------------------------------------------------
