@@ -3,6 +3,11 @@ in-tree next to this file (kvpath/libkvpath.so), where `kvpath._lib` loads it.
 
     python -m kvpath.build          # from research-2_amd/, or via __graft_entry__.build()
 
+Each source is also compiled to gfx950 assembly with the same flags, and the assembly is scanned
+(kvpath.isa_scan) for any instruction that touches a register an inline-asm load may still be
+writing; a report refuses the link. (The attention kernels issue loads the compiler does not
+track; a register copied or reused before its wait once faulted the GPU.)
+
 hipcc cross-compiles without a GPU, so this runs anywhere ROCm is installed.
 """
 
@@ -54,14 +59,51 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def assemble(src: Path, out: Path | None = None) -> Path:
+    """The gfx950 assembly of one source, with the library's own flags."""
+    out = out or BUILD_DIR / (src.stem + ".s")
+    cmd = [hipcc(), *HIP_FLAGS, "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src.name}:\n{proc.stderr}")
+    return out
+
+
+class IsaHazardError(RuntimeError):
+    """The assembly has an instruction that touches an outstanding inline-asm load's register."""
+
+
+def refuse_hazards(assembly: dict[str, str]) -> None:
+    """Scan each source's assembly ({name: text}); raise IsaHazardError on any report."""
+    from kvpath import isa_scan
+
+    found = {}
+    for name, text in assembly.items():
+        for kernel, reports in isa_scan.scan(text).items():
+            if reports:
+                found[f"{name}:{kernel}"] = reports
+    if found:
+        lines = [f"{k}: {len(v)} report(s), first: {v[0]}" for k, v in found.items()]
+        raise IsaHazardError("inline-asm load destinations touched before their wait; "
+                             "not linking libkvpath.so:\n" + "\n".join(lines))
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip and link libkvpath.so. Always recompiles (it is the build check)."""
+    """Compile every csrc/*.hip, scan its assembly, and link libkvpath.so. Always recompiles (it
+    is the build check)."""
     BUILD_DIR.mkdir(exist_ok=True)
     srcs = sources()
     assert srcs, f"no HIP sources under {CSRC}"
-    workers = min(len(srcs), max(1, (os.cpu_count() or 1)))
+    workers = min(2 * len(srcs), max(1, (os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
-        objs = list(pool.map(_compile, srcs))
+        objs_f = [pool.submit(_compile, src) for src in srcs]
+        asm_f = [pool.submit(assemble, src) for src in srcs]
+        objs = [f.result() for f in objs_f]
+        asms = [f.result() for f in asm_f]
+    refuse_hazards({path.name: path.read_text() for path in asms})
+    if verbose:
+        print(f"scanned the assembly of {len(asms)} sources: no outstanding-load hazards",
+              flush=True)
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]
