@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int ch
         const int n = s_len[li];
         const uint64_t written = s_written[li];
         const bool fresh = written & 1ull;
-        const int64_t page = static_cast<int64_t>(a.slots[t0]) / block;
+        const int64_t page = s_slot[t0 - c0 + 1] / block;
         const uint16_t* src = static_cast<const uint16_t*>(m ? a.v : a.k) +
                               h * (m ? a.v_shead : a.k_shead) + 8 * lane;
         const int64_t s_row = m ? a.v_srow : a.k_srow;
@@ -175,7 +175,8 @@ __global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int ch
         u32x4 keep[kKeep];
 #pragma unroll
         for (int j = 0; j < kKeep; ++j)
-            keep[j] = j < n ? *reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row) : u32x4{0, 0, 0, 0};
+            keep[j] = j < n ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row))
+                            : u32x4{0, 0, 0, 0};
         const float s_stored = *scale_slot;
         float amax = 0.0f;
 #pragma unroll
@@ -216,14 +217,20 @@ __global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int ch
             }
         }
 
-        // Pass 2: the run's rows, x * r_new.
+        // Pass 2: the run's rows, x * r_new. (The kept rows pass through an empty asm first, so
+        // they are widened again here from their packed bf16 rather than pass 1's f32 copies
+        // being held in registers across the requantization.)
+#pragma unroll
+        for (int j = 0; j < kKeep; ++j) asm volatile("" : "+v"(keep[j]));
 #pragma unroll
         for (int j = 0; j < kKeep; ++j) {
             if (j < n) {
                 float x[8];
                 widen_bf16x8(keep[j], x);
-                const int64_t row = static_cast<int64_t>(a.slots[t0 + j]) - page * block;
-                *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) = quantize8(x, r_new);
+                // The first kKeep rows of a run that starts in the chunk lie in the LDS window.
+                const int64_t row = s_slot[t0 - c0 + 1 + j] - page * block;
+                __builtin_nontemporal_store(quantize8(x, r_new),
+                                            reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row));
             }
         }
         for (int j = kKeep; j < n; ++j) {

@@ -357,6 +357,27 @@ def _fake_fp8(q, k, v, kv_member, row_request, positions, query_start_loc, seq_l
     return torch.empty(q.shape[0], q.shape[1] * q.shape[2], dtype=q.dtype, device=q.device)
 
 
+def _backward(ctx, *grads):
+    """The op is inference-only, as kelpie's is (ops/paged_attention.py:380-385): a backward
+    raises, naming that, instead of failing as a missing autograd formula."""
+    del ctx, grads
+    raise NotImplementedError("kvpath::paged_attention has no backward: the paged-KV path is "
+                              "inference-only (kelpie defers training to its train-step branch)")
+
+
+def _setup_context(ctx, inputs, output) -> None:
+    del ctx, inputs, output
+
+
+# torch.library refuses register_autograd on an op that mutates an argument (kv_member), the same
+# wall kelpie's op registry meets and answers by keeping the raising backward on its own op
+# object (kernels/op.py:101-113). Here the backward is given to the op's generated autograd
+# function directly: it only ever raises, so no gradient semantics of the mutation are implied.
+for _op in (paged_attention, paged_attention_fp8):
+    _op._backward_fn = _backward
+    _op._setup_context_fn = _setup_context
+
+
 def kv_gather(kv_member: torch.Tensor, block_table: torch.Tensor, width: int | None = None
               ) -> tuple[torch.Tensor, torch.Tensor]:
     """The gather inside _attend (ops/paged_attention.py:172-177): K and V of every entry's first

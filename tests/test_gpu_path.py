@@ -135,6 +135,41 @@ def test_gather_bit_exact() -> None:
     assert torch.equal(gv.cpu().view(torch.int16), wv.view(torch.int16))
 
 
+@pytest.mark.parametrize("dtype,heads,dim", [(torch.float32, 4, 128),
+                                             (torch.float8_e4m3fn, 8, 128),
+                                             (torch.bfloat16, 2, 64)])
+def test_gather_dtypes_strides_and_bad_ids(dtype, heads, dim) -> None:
+    """Gather from f32, fp8 and bf16 members, through a block table that is a column slice of a
+    wider one (row stride > width), with a null page, a page id past the pool and a negative id
+    in it: bit-exact against the oracle; an id outside the pool gives zeros."""
+    say("gather", dtype, heads, dim)
+    pages, block = 96, 16
+    member = _engine_member(pages, block, heads, dim,
+                            torch.uint8 if dtype == torch.float8_e4m3fn else dtype)
+    if dtype == torch.float8_e4m3fn:
+        g = torch.Generator().manual_seed(4)
+        member.copy_(torch.randint(0, 126, member.shape, generator=g, dtype=torch.uint8).cuda())
+        member = member.view(torch.float8_e4m3fn)
+    else:
+        _random_fill(member, 4)
+    g = torch.Generator().manual_seed(5)
+    wide = torch.randint(1, pages, (5, 40), generator=g, dtype=torch.int32)
+    wide[0, 3] = 0            # the null page
+    wide[1, 0] = pages + 3    # past the pool
+    wide[2, 5] = -7           # negative
+    table = wide.cuda()[:, :12]  # row stride 40, width 12
+    assert table.stride(0) == 40
+    gk, gv = kvpath.kv_gather(member, table)
+    ref = compact_member(member)
+    wk, wv = kvbytes.kv_gather(ref, table.cpu(), 12)
+    bits = torch.uint8 if dtype == torch.float8_e4m3fn else (
+        torch.int32 if dtype == torch.float32 else torch.int16)
+    assert torch.equal(gk.cpu().view(bits), wk.view(bits))
+    assert torch.equal(gv.cpu().view(bits), wv.view(bits))
+    assert not bool(gk[1, :block].cpu().view(bits).any())  # the page past the pool: zeros
+    assert not bool(gv[2, 5 * block:6 * block].cpu().view(bits).any())
+
+
 def compact_member(kv_member: torch.Tensor) -> torch.Tensor:
     """The whole member on the CPU, in a fresh arena-layout view."""
     pages, _, block, heads, dim = kv_member.shape

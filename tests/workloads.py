@@ -262,3 +262,53 @@ def copy_pairs(step: Step, n: int, seed: int = 0) -> tuple[torch.Tensor, torch.T
     dst = free[torch.randperm(free.numel(), generator=g)[:n]].to(torch.int32)
     device = step.kv_member.device
     return src.to(device), dst.to(device)
+
+
+# ---- the reference's per-op case list --------------------------------------------------------
+
+GPT_OSS_ATTN = dict(heads=64, kv_heads=8, head_dim=64, block=16)
+
+
+def reference_cases() -> list[tuple[str, Batch]]:
+    """The shapes kelpie's per-op proof grades `paged_attention` on (kelpie/scripts/
+    bench_attention.py:42-91): gpt-oss-20b attention (64 q / 8 kv heads, D 64, block 16, sinks)
+    at the build's step families for max_seq_len 512, 8 requests, 1024 batch tokens -- decode
+    R = 1..8 (and 5 real entries padded to 8), prefill T = 1..1024 (fresh prompts split over
+    512-row entries, a chunk after 300 cached keys, mixed prefill and decode), decode_extra R x 16
+    (DFlash's 1 + 15 rows; full and ragged) -- each with windows 0 and 128, and the drafter's
+    non-causal, sink-free call at the decode_extra shapes. Contexts come from random.Random(0) in
+    the reference's draw order, so the shapes are the reference's own; case i is drawn with
+    seed i, as the reference draws it."""
+    import random
+
+    rng = random.Random(0)
+    max_seq, k_extra, decode = 512, 15, (1, 2, 4, 8)
+    shapes: list[tuple[str, dict]] = []
+    for r in decode:
+        shapes.append((f"decode R={r}", dict(entries=[(rng.randint(1, 700), 1) for _ in range(r)],
+                                             tokens=r, reqs=r)))
+    shapes.append(("decode R=8 (5 real)",
+                   dict(entries=[(rng.randint(1, 700), 1) for _ in range(5)], tokens=8, reqs=8)))
+    for t in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024):
+        n = -(-t // max_seq)
+        shapes.append((f"prefill T={t} fresh", dict(entries=[(0, t // n)] * n, tokens=t, reqs=n)))
+    shapes.append(("prefill T=512 chunk@300", dict(entries=[(300, 512)], tokens=512, reqs=1)))
+    shapes.append(("prefill T=128 mixed", dict(entries=[(0, 57), (400, 1), (33, 1), (129, 40),
+                                                        (5, 3)], tokens=128, reqs=8)))
+    shapes.append(("prefill T=1024 mixed", dict(entries=[(0, 300), (700, 1), (250, 511),
+                                                         (20, 100)], tokens=1024, reqs=8)))
+    for r in decode:
+        w = 1 + k_extra
+        full = [(rng.randint(1, 600), w) for _ in range(r)]
+        shapes.append((f"decode_extra R={r}", dict(entries=full, tokens=r * w, reqs=r)))
+        ragged = [(rng.randint(1, 600), 1 + rng.randint(0, k_extra)) for _ in range(r)]
+        shapes.append((f"decode_extra R={r} ragged", dict(entries=ragged, tokens=r * w, reqs=r)))
+    cases = []
+    for label, kw in shapes:
+        kw = {**kw, "entries": tuple(tuple(e) for e in kw["entries"])}
+        for window in (0, 128):
+            cases.append((f"{label} w{window}", Batch(**kw, window=window, **GPT_OSS_ATTN)))
+        if label.startswith("decode_extra"):
+            cases.append((f"{label} drafter", Batch(**kw, sinks=False, causal=False,
+                                                    **GPT_OSS_ATTN)))
+    return cases
