@@ -25,6 +25,8 @@
  *   kvpath_split_plan         no counterpart in kelpie's op (it does not split a row's keys); the
  *                             per-sequence split follows kernels/vendored/cuda/vllm_attention/
  *                             triton_unified_attention.py:335-355
+ *   kvpath_paged_attention_noalloc  no counterpart: the whole op for callers that cannot
+ *                             allocate (see its declaration)
  */
 #ifndef KVPATH_H
 #define KVPATH_H
@@ -220,6 +222,21 @@ int32_t kvpath_paged_attention(const kvpath_rows* q, const kvpath_rows* k, const
                                const kvpath_cache* cache, const kvpath_plan* plan,
                                const kvpath_attn_opts* opts, kvpath_rows* out, void* workspace,
                                int64_t workspace_bytes, kvpath_stream_t stream);
+
+/*
+ * The whole op without a workspace argument.  No counterpart in the reference: it is for callers
+ * that cannot allocate -- code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments and results as kvpath_paged_attention; the split-KV partials go to
+ * the library's own 64 MiB device scratch (one per GPU, held until the process ends), so a step
+ * whose kvpath_workspace_bytes exceeds 64 MiB is refused with KVPATH_EINVAL before any device
+ * call.  No memory is allocated.  Every call on a GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (on different streams, or from different threads) race and must not.  The
+ * scratch keeps the last call's partials; nothing in it needs to start at zero.
+ */
+int32_t kvpath_paged_attention_noalloc(const kvpath_rows* q, const kvpath_rows* k,
+                                       const kvpath_rows* v, const kvpath_cache* cache,
+                                       const kvpath_plan* plan, const kvpath_attn_opts* opts,
+                                       kvpath_rows* out, kvpath_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -6,11 +6,43 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "kvpath_internal.h"
 
 namespace {
+
+// ---- the no-allocation entry point's scratch ---------------------------------------------------
+
+// Split-KV partials of kvpath_paged_attention_noalloc: one file-scope device array, which each GPU
+// the library runs on holds (64 MiB) until the process ends. Host code never passes `scratch`
+// itself to a kernel or a copy -- in host code the name is a stand-in, not a device address --
+// only the address hipGetSymbolAddress returns for the current device (scratch_ptr below).
+constexpr int64_t kScratchBytes = int64_t{64} << 20;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device (with that device
+// current) and kept. Returns a HIP error when the device or the lookup fails.
+hipError_t scratch_ptr(void** out) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 thread_local std::string g_error;
 
@@ -275,6 +307,36 @@ int32_t attend_args(const kvpath_rows* q, const kvpath::CacheView& c, const kvpa
     return ok();
 }
 
+// The whole op over a given workspace: validate the attention half before the append launches,
+// so a refused call writes nothing; fuse the append into the partition kernels when they take it.
+int32_t paged_attention_impl(const kvpath_rows* q, const kvpath_rows* k, const kvpath_rows* v,
+                             const kvpath_cache* cache, const kvpath_plan* plan,
+                             const kvpath_attn_opts* opts, kvpath_rows* out, void* workspace,
+                             int64_t workspace_bytes, kvpath_stream_t stream, const char* what) {
+    kvpath::CacheView c;
+    int32_t st = check_cache(cache, what, &c);
+    if (st != KVPATH_OK) return st;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    kvpath::AttnArgs a;
+    if ((st = attend_args(q, c, plan, opts, out, workspace, workspace_bytes, what, &a)) != KVPATH_OK)
+        return st;
+    kvpath::AppendArgs ap;
+    if ((st = append_args(c, k, v, plan, what, &ap)) != KVPATH_OK) return st;
+    if (a.T > 0 && append_fuses(ap, a)) {
+        // One launch: the partitions that hold this step's rows write them.
+        a.k_new = ap.k;
+        a.v_new = ap.v;
+        a.kn_srow = ap.k_srow;
+        a.kn_shead = ap.k_shead;
+        a.vn_srow = ap.v_srow;
+        a.vn_shead = ap.v_shead;
+        a.slots = ap.slots;
+    } else if ((st = append_launch(ap, s, what)) != KVPATH_OK) {
+        return st;
+    }
+    return launched(kvpath::launch_attention(a, s), what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -406,30 +468,37 @@ int32_t kvpath_paged_attention(const kvpath_rows* q, const kvpath_rows* k, const
                                const kvpath_cache* cache, const kvpath_plan* plan,
                                const kvpath_attn_opts* opts, kvpath_rows* out, void* workspace,
                                int64_t workspace_bytes, kvpath_stream_t stream) {
-    kvpath::CacheView c;
-    int32_t st = check_cache(cache, "paged_attention", &c);
-    if (st != KVPATH_OK) return st;
-    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // Validate the attention half before the append launches, so a refused call writes nothing.
-    kvpath::AttnArgs a;
-    if ((st = attend_args(q, c, plan, opts, out, workspace, workspace_bytes, "paged_attention", &a)) !=
-        KVPATH_OK)
-        return st;
-    kvpath::AppendArgs ap;
-    if ((st = append_args(c, k, v, plan, "paged_attention", &ap)) != KVPATH_OK) return st;
-    if (a.T > 0 && append_fuses(ap, a)) {
-        // One launch: the partitions that hold this step's rows write them.
-        a.k_new = ap.k;
-        a.v_new = ap.v;
-        a.kn_srow = ap.k_srow;
-        a.kn_shead = ap.k_shead;
-        a.vn_srow = ap.v_srow;
-        a.vn_shead = ap.v_shead;
-        a.slots = ap.slots;
-    } else if ((st = append_launch(ap, s, "paged_attention")) != KVPATH_OK) {
-        return st;
-    }
-    return launched(kvpath::launch_attention(a, s), "paged_attention");
+    return paged_attention_impl(q, k, v, cache, plan, opts, out, workspace, workspace_bytes, stream,
+                                "paged_attention");
+}
+
+int32_t kvpath_paged_attention_noalloc(const kvpath_rows* q, const kvpath_rows* k,
+                                       const kvpath_rows* v, const kvpath_cache* cache,
+                                       const kvpath_plan* plan, const kvpath_attn_opts* opts,
+                                       kvpath_rows* out, kvpath_stream_t stream) {
+    const char* what = "paged_attention_noalloc";
+    // The step's workspace size first, from the shapes alone: a step that needs more than the
+    // scratch holds is refused before any device call.
+    if (q == nullptr || cache == nullptr || plan == nullptr)
+        return fail(KVPATH_EINVAL, "%s: null argument", what);
+    const int64_t need = kvpath_workspace_bytes(plan->num_tokens, plan->num_reqs, q->heads,
+                                                cache->num_kv_heads, cache->head_dim,
+                                                plan->table_width, cache->block_size,
+                                                opts ? opts->partition_tokens : 0);
+    if (need < 0)
+        return fail(KVPATH_EINVAL, "%s: a shape the library refuses (see kvpath_workspace_bytes)",
+                    what);
+    if (need > kScratchBytes)
+        return fail(KVPATH_EINVAL,
+                    "%s: this step needs %lld bytes of split-KV scratch, more than the %lld the "
+                    "no-allocation entry point holds; call kvpath_paged_attention with a workspace",
+                    what, (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    const hipError_t err = scratch_ptr(&ws);
+    if (err != hipSuccess)
+        return fail(KVPATH_ELAUNCH, "%s: the scratch's device address: %s", what,
+                    hipGetErrorString(err));
+    return paged_attention_impl(q, k, v, cache, plan, opts, out, ws, kScratchBytes, stream, what);
 }
 
 }  // extern "C"

@@ -28,6 +28,7 @@ EXPORTS = (
     "kvpath_attend_partitions",
     "kvpath_attend_reduce",
     "kvpath_paged_attention",
+    "kvpath_paged_attention_noalloc",
 )
 
 
@@ -131,6 +132,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         "kvpath_paged_attention": (
             i32, [p(Rows), p(Rows), p(Rows), p(Cache), p(Plan), p(AttnOpts), p(Rows), vp, i64,
                   vp]),
+        "kvpath_paged_attention_noalloc": (
+            i32, [p(Rows), p(Rows), p(Rows), p(Cache), p(Plan), p(AttnOpts), p(Rows), vp]),
     }
     assert tuple(sigs) == EXPORTS
     for name, (restype, argtypes) in sigs.items():
