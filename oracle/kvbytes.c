@@ -21,11 +21,12 @@
  *                                      s_old * 2^k          when t > s_old > 0, k >= 1 the
  *                                                           smallest with s_old * 2^k >= t
  *                                      s_old                otherwise
- *                              r_new = 1 / s_new (0 when s_new == 0)
+ *                              r_new = 1 / s_new (0 when s_new == 0, and when s_new == inf)
  *                              if k > 0: every row the step does not write becomes
  *                                e4m3(clamp(f32(q) * 2^-k, +-448)), exact unless it falls below
  *                                e4m3's normals (the clamp only turns a stale NaN byte into -448)
- *                              each written row becomes e4m3(clamp(x * r_new, +-448));
+ *                              each written row becomes e4m3(clamp(x * r_new, +-448)), or 0
+ *                                when r_new == 0 (a run of zeros, or one holding an inf);
  *                              scale = s_new.
  *                            A fresh page's largest element is stored exactly (it maps to 448);
  *                            a scale only ever grows by a power of two, so requantizing the rows

@@ -10,11 +10,12 @@
 //        s_old  = fresh ? 0 : scale[page, m, h]
 //        s_new  = t when s_old = 0; s_old * 2^k when t > s_old > 0, k >= 1 the smallest with
 //                 s_old * 2^k >= t; s_old otherwise
-//        r_new  = 1 / s_new (0 when s_new = 0)
+//        r_new  = 1 / s_new (0 when s_new = 0, and when s_new = inf)
 //      When the scale grew (k > 0), every row of the page the run does not write is requantized
 //      as q' = e4m3(clamp(f32(q) * 2^-k, +-448)) -- an exponent shift, exact unless the value
 //      drops below e4m3's normals. Each run row is quantized as q = e4m3(clamp(x * r_new,
-//      +-448)), and scale[page, m, h] = s_new.
+//      +-448)), or q = 0 when r_new = 0 (a run of zeros, or one holding an inf), and
+//      scale[page, m, h] = s_new.
 // A fresh page's largest element maps to 448; growth by powers of two keeps the e4m3 rounding of
 // a decode stream (a row appended per step, the scale growing on many of them) from compounding.
 // Products and quotients are single IEEE-754 binary32 operations rounded to nearest even; the
@@ -87,6 +88,35 @@ __device__ __forceinline__ u32x2 quantize8(const float (&x)[8], float r) {
     int hi = cvt2_fp8<false>(x[4] * r, x[5] * r, 0);
     hi = cvt2_fp8<true>(x[6] * r, x[7] * r, hi);
     return u32x2{static_cast<uint32_t>(lo), static_cast<uint32_t>(hi)};
+}
+
+// Eight values times r as eight e4m3 bytes, for a run whose inputs are all finite: then
+// |x * r| <= 448 (1 + 3 * 2^-24) < 464 (r rounds 1 / s_new with s_new >= absmax / 448), which the
+// conversion rounds to at most 448, so the clamp of quantize8 changes no result and is left out.
+__device__ __forceinline__ u32x2 quantize8_finite(const float (&x)[8], float r) {
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[0] * r, x[1] * r, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[2] * r, x[3] * r, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[4] * r, x[5] * r, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[6] * r, x[7] * r, hi, true);
+    return u32x2{static_cast<uint32_t>(lo), static_cast<uint32_t>(hi)};
+}
+
+// Eight run values as stored: zeros when r = 0, else the finite or the clamped conversion.
+// (r and finite are uniform over the unit's lanes.)
+__device__ __forceinline__ u32x2 quantize_run8(const float (&x)[8], float r, bool finite) {
+    if (!(r > 0.0f)) return u32x2{0, 0};
+    return finite ? quantize8_finite(x, r) : quantize8(x, r);
+}
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// The running maximum of |x| over 16 bytes of bf16, as bit patterns: with the sign bit cleared a
+// bf16 orders as its 16-bit pattern (zeros, subnormals, normals, then inf at 0x7f80 and NaNs
+// above), so two values take one packed integer maximum.
+__device__ __forceinline__ u16x2 absmax_bits(u16x2 m, u32x4 w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
+    return m;
 }
 
 // Eight bf16 (16 bytes) as eight f32, exact.
@@ -178,20 +208,28 @@ __global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int ch
             keep[j] = j < n ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row))
                             : u32x4{0, 0, 0, 0};
         const float s_stored = *scale_slot;
-        float amax = 0.0f;
+        u16x2 mb = {0, 0};
 #pragma unroll
-        for (int j = 0; j < kKeep; ++j) {
-            float x[8];
-            widen_bf16x8(keep[j], x);
-            amax = fmaxf(amax, absmax8(x));
-        }
-        for (int j = kKeep; j < n; ++j) {
-            float x[8];
-            widen_bf16x8(*reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row), x);
-            amax = fmaxf(amax, absmax8(x));
-        }
+        for (int j = 0; j < kKeep; ++j) mb = absmax_bits(mb, keep[j]);
+        for (int j = kKeep; j < n; ++j)
+            mb = absmax_bits(mb, *reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row));
+        uint32_t bits = max(static_cast<uint32_t>(mb[0]), static_cast<uint32_t>(mb[1]));
 #pragma unroll
-        for (int o = L / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, L));
+        for (int o = L / 2; o >= 1; o >>= 1) bits = max(bits, static_cast<uint32_t>(__shfl_xor(static_cast<int>(bits), o, L)));
+        // All finite (the usual case): the bit maximum is the absmax. An inf or NaN takes the f32
+        // rule (fmaxf skips NaNs) and the clamped conversion.
+        const bool finite = bits < 0x7f80u;
+        float amax = __uint_as_float(bits << 16);
+        if (!finite) {
+            amax = 0.0f;
+            for (int j = 0; j < n; ++j) {
+                float x[8];
+                widen_bf16x8(*reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row), x);
+                amax = fmaxf(amax, absmax8(x));
+            }
+#pragma unroll
+            for (int o = L / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, L));
+        }
 
         int k;
         const float s_new = grow_scale(fresh ? 0.0f : s_stored, __fdiv_rn(amax, kFp8Max), k);
@@ -229,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int ch
                 widen_bf16x8(keep[j], x);
                 // The first kKeep rows of a run that starts in the chunk lie in the LDS window.
                 const int64_t row = s_slot[t0 - c0 + 1 + j] - page * block;
-                __builtin_nontemporal_store(quantize8(x, r_new),
+                __builtin_nontemporal_store(quantize_run8(x, r_new, finite),
                                             reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row));
             }
         }
@@ -237,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void append_fp8_runs(AppendArgs a, int ch
             float x[8];
             widen_bf16x8(*reinterpret_cast<const u32x4*>(src + (t0 + j) * s_row), x);
             const int64_t row = static_cast<int64_t>(a.slots[t0 + j]) - page * block;
-            *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) = quantize8(x, r_new);
+            *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) = quantize_run8(x, r_new, finite);
         }
         if (lane == 0) *scale_slot = s_new;
     }
@@ -294,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void append_fp8_generic(AppendArgs a) {
             uint8_t* p = cache + head_base + (a.slots[r] - page * a.c.block) * a.c.s_row;
             for (int d = lane; d < a.c.d; d += kGroup) {
                 const float x = load_as_f32(src, r * s_row + h * s_head + d, a.in_dt);
-                p[d] = f32_to_fp8(__fmul_rn(x, r_new));
+                p[d] = r_new > 0.0f ? f32_to_fp8(__fmul_rn(x, r_new)) : 0;
             }
         }
         if (lane == 0) *scale_slot = s_new;

@@ -290,6 +290,51 @@ def test_fp8_append_prefill_sized_bit_exact(offset) -> None:
     assert torch.equal(scale.cpu()[1:], ref_scale[1:])
 
 
+@pytest.mark.parametrize("rows", [48, 34000])
+def test_fp8_append_non_finite_rows_bit_exact(rows) -> None:
+    """Rows holding +-inf or NaN in some (member, head) runs, among finite ones, in decode-sized
+    and prefill-sized steps: the run kernel takes such a run through the f32 absmax (NaN skipped)
+    and the clamped conversion, the rest through its finite path, and an inf scale stores zeros;
+    then a second step appends a row after each decode row, an inf among them growing a finite
+    scale (the requantization's shift runs to the overflow). Bytes and scale bits equal the C
+    oracle's after each step."""
+    say("fp8 append non-finite rows", rows)
+    pages, block, heads, dim = 2400, 16, 8, 128
+    kv = _engine_member(pages, block, heads, dim, torch.uint8).view(torch.float8_e4m3fn)
+    g = torch.Generator().manual_seed(29)
+    kv.view(torch.uint8).copy_(torch.randint(0, 120, kv.shape, generator=g, dtype=torch.uint8).cuda())
+    scale = (torch.rand(pages, 2, heads, generator=g) * 0.05).cuda()
+    ref_kv = compact_member(kv)
+    ref_scale = scale.cpu().clone()
+    order = (torch.randperm(pages - 1, generator=g) + 1)
+    pos = torch.arange(rows) * (1 if rows > 1000 else 16)  # decode-sized: one row per page
+    slots = (order[pos // block] * block + pos % block).to(torch.int32)
+    k = torch.randn(rows, heads, dim, generator=g)
+    v = torch.randn(rows, heads, dim, generator=g)
+    k[3, 2, 5] = float("inf")
+    k[7, 0, 100] = float("-inf")
+    v[3, 5, 9] = float("nan")
+    k[40, 1, 0] = float("nan")
+    v[41, 7, 127] = float("inf")
+
+    def step(k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor) -> None:
+        k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+        kvbytes.kv_append_fp8(ref_kv, ref_scale, k, v, slots)
+        kvpath.write_kv(kv, k.cuda(), v.cuda(), slots.cuda(), scale)
+        torch.cuda.synchronize()
+        assert torch.equal(compact_member(kv)[1:].contiguous().view(torch.uint8),
+                           ref_kv[1:].contiguous().view(torch.uint8))
+        assert torch.equal(scale.cpu()[1:].view(torch.int32), ref_scale[1:].view(torch.int32))
+
+    step(k, v, slots)
+    if rows < 1000:
+        k2 = torch.randn(rows, heads, dim, generator=g)
+        v2 = torch.randn(rows, heads, dim, generator=g)
+        k2[10, 4, 7] = float("inf")
+        v2[11, 2, 2] = float("nan")
+        step(k2, v2, slots + 1)
+
+
 # ---- attention: golden cases and the configurations ---------------------------------------------------
 
 
