@@ -260,14 +260,14 @@ def test_fp8_append_bit_exact_over_steps(dim, in_dtype) -> None:
     step([4, 0, 20])      # multi-row step across a page boundary
 
 
-@pytest.mark.parametrize("offset", [0, 5])
-def test_fp8_append_prefill_sized_bit_exact(offset) -> None:
+@pytest.mark.parametrize("offset,dim", [(0, 128), (5, 128), (0, 64)])
+def test_fp8_append_prefill_sized_bit_exact(offset, dim) -> None:
     """Prefill-sized fp8 appends (34,000 rows: the run kernel's 16-row chunks) starting at a page
-    boundary or mid-page (runs then straddle the chunks), with stale bytes and scales, and a
-    last row whose slot lies outside the pool: bytes and scales equal the C oracle's. (A step's
-    rows that share a page are consecutive, as in every kelpie plan.)"""
-    say("fp8 append prefill-sized, offset", offset)
-    pages, block, heads, dim = 2400, 16, 8, 128
+    boundary or mid-page (runs then straddle the chunks), at D 128 and 64, with stale bytes and
+    scales, and a last row whose slot lies outside the pool: bytes and scales equal the C
+    oracle's. (A step's rows that share a page are consecutive, as in every kelpie plan.)"""
+    say("fp8 append prefill-sized, offset", offset, "dim", dim)
+    pages, block, heads = 2400, 16, 8
     kv = _engine_member(pages, block, heads, dim, torch.uint8).view(torch.float8_e4m3fn)
     g = torch.Generator().manual_seed(11 + offset)
     kv.view(torch.uint8).copy_(torch.randint(0, 120, kv.shape, generator=g, dtype=torch.uint8).cuda())
