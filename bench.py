@@ -147,6 +147,93 @@ def time_graph(fn, rotations: list, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+# The reference's published microseconds per layer for its buckets (kelpie/NOTES-attn.md:44-49:
+# gpt-oss attention, decode-shaped steps as graph replays, prefill eager), on A100 and H100, for
+# its reference op and for vLLM's Triton kernel. Context beside the figures measured here, not a
+# target. Keys are this bench's bucket labels (NOTES: "decode_extra R=8 x16 w0" is the full
+# decode_extra R=8 bucket, "prefill T=128 w0" the fresh prefill).
+PUBLISHED_US = {
+    "decode R=1 w0": {"A100 ref": 79.9, "A100 vllm": 24.6, "H100 ref": 63.1, "H100 vllm": 19.8},
+    "decode R=8 w0": {"A100 ref": 209.9, "A100 vllm": 34.8, "H100 ref": 148.7, "H100 vllm": 25.5},
+    "decode R=8 w128": {"A100 ref": 215.0, "A100 vllm": 22.5, "H100 ref": 153.5, "H100 vllm": 18.1},
+    "decode_extra R=8 w0": {"A100 ref": 1946.6, "A100 vllm": 51.2, "H100 ref": 1259.2,
+                            "H100 vllm": 35.2},
+    "prefill T=128 fresh w0": {"A100 ref": 1031, "A100 vllm": 250, "H100 ref": 738,
+                               "H100 vllm": 158},
+    "prefill T=1024 fresh w0": {"A100 ref": 13451, "A100 vllm": 360, "H100 ref": 8998,
+                                "H100 vllm": 232},
+}
+CASE_REPLAYS = 50
+CASE_WARMUP = 5
+
+
+def time_call(fn, args: tuple, graphed: bool) -> float:
+    """Median microseconds of one call over CASE_REPLAYS, as the reference times its buckets
+    (bench_attention.py:189-208): one call captured in a hipGraph and replayed, HIP events around
+    each replay; or, eagerly, HIP events around each call."""
+    import torch
+
+    fn(*args)
+    torch.cuda.synchronize()
+    if graphed:
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
+            fn(*args)
+        torch.cuda.current_stream().wait_stream(stream)
+        run = graph.replay
+    else:
+        def run() -> None:
+            fn(*args)
+    for _ in range(CASE_WARMUP):
+        run()
+    times = []
+    for _ in range(CASE_REPLAYS):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        run()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end) * 1e3)
+    return statistics.median(times)
+
+
+def reference_buckets_line() -> dict:
+    """Microseconds per layer for the reference's timing buckets (workloads.reference_buckets),
+    each drawn by the reference's generator with seed 20 as it draws them, the published A100 /
+    H100 figures beside the six buckets kelpie/NOTES-attn.md lists."""
+    import torch
+
+    import kvpath
+    from kvpath import _lib
+    from reference_sample import sample
+    from workloads import reference_buckets
+
+    _lib.load()  # fails loudly without the HIP library
+    rows = []
+    for label, batch, graphed in reference_buckets():
+        args = sample(batch, "cuda", torch.bfloat16, seed=20)
+        us = time_call(kvpath.paged_attention, args, graphed)
+        row = {"bucket": label, "us_per_layer": round(us, 2), "timing": "graph" if graphed else "eager",
+               "rows": batch.n_rows, "tokens": batch.tokens}
+        if label in PUBLISHED_US:
+            row["published_us"] = PUBLISHED_US[label]
+        rows.append(row)
+        log(f"{label}: {us:.2f} us ({row['timing']})")
+        del args
+        torch.cuda.empty_cache()
+    # The same timing of one trivial kernel (a one-element add): the launch floor every bucket
+    # carries, graphed and eager.
+    one = torch.zeros(1, device="cuda")
+    floor = {"graph_us": round(time_call(lambda x: x.add_(1), (one,), True), 2),
+             "eager_us": round(time_call(lambda x: x.add_(1), (one,), False), 2)}
+    return {"mode": "reference_buckets", "unit": "us per layer (gpt-oss attention: 64 q / 8 kv "
+            "heads, D 64, block 16, sinks; append + attention, one op call)", "n_gpus": 1,
+            "published": "kelpie/NOTES-attn.md:44-49 (A100/H100; context, not a target)",
+            "launch_floor": floor, "rows": rows}
+
+
 def measured_traffic(kernel: str, workload: str) -> int | None:
     """HBM bytes per launch of `kernel` on `workload` from the committed rocprofv3 counter
     summary (FETCH_SIZE scaled by its copy-kernel calibration, plus WRITE_SIZE), or None when
@@ -420,6 +507,10 @@ def main() -> int:
                          "the batch needs)")
     ap.add_argument("--members", type=int, default=2,
                     help="layers in the arena's unit (the row stride spans them all)")
+    ap.add_argument("--cases", action="store_true",
+                    help="instead of the configs: microseconds per layer for the reference's "
+                         "timing buckets (kelpie/scripts/bench_attention.py), with its published "
+                         "A100/H100 figures beside them")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU; the paged-KV "
@@ -430,6 +521,9 @@ def main() -> int:
     import torch
 
     torch.cuda.set_device(0)
+    if args.cases:
+        print(json.dumps(reference_buckets_line()), flush=True)
+        return 0
     cfg = args.config or CONFIG
     res = measure(cfg, args, extras=True)
     line = {

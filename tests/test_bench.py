@@ -103,3 +103,23 @@ def test_split_bytes_count_partitions_per_entry() -> None:
     counts = [min(9, -(-n // 512)) for n in lens]
     parts = sum(32 * c for c in counts) * (128 * 2 + 8)
     assert b["reduce"] == parts + len(lens) * 32 * 128 * 2
+
+
+def test_published_buckets_are_timed() -> None:
+    """Every bucket the reference publishes microseconds for (kelpie/NOTES-attn.md:44-49) is one
+    `bench.py --cases` times, at the reference's shapes: decode R=1 is one row over one entry,
+    decode_extra R=8 is 8 entries of 16 rows, the prefills are fresh prompts of 128 and 1024
+    rows in 512-row entries; decode-shaped buckets are graph replays, prefill eager."""
+    from workloads import reference_buckets
+
+    buckets = {label: (batch, graphed) for label, batch, graphed in reference_buckets()}
+    assert len(buckets) == 46
+    assert set(bench.PUBLISHED_US) <= set(buckets)
+    batch, graphed = buckets["decode R=1 w0"]
+    assert (batch.n_rows, len(batch.entries), graphed) == (1, 1, True)
+    batch, graphed = buckets["decode_extra R=8 w0"]
+    assert [rows for _, rows in batch.entries] == [16] * 8 and graphed
+    batch, graphed = buckets["prefill T=1024 fresh w0"]
+    assert batch.entries == ((0, 512), (0, 512)) and not graphed
+    batch, _ = buckets["decode R=8 w128"]
+    assert batch.window == 128 and (batch.heads, batch.kv_heads, batch.head_dim) == (64, 8, 64)

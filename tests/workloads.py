@@ -269,19 +269,9 @@ def copy_pairs(step: Step, n: int, seed: int = 0) -> tuple[torch.Tensor, torch.T
 GPT_OSS_ATTN = dict(heads=64, kv_heads=8, head_dim=64, block=16)
 
 
-def reference_cases() -> list[tuple[str, Batch]]:
-    """The shapes kelpie's per-op proof grades `paged_attention` on (kelpie/scripts/
-    bench_attention.py:42-91): gpt-oss-20b attention (64 q / 8 kv heads, D 64, block 16, sinks)
-    at the build's step families for max_seq_len 512, 8 requests, 1024 batch tokens -- decode
-    R = 1..8 (and 5 real entries padded to 8), prefill T = 1..1024 (fresh prompts split over
-    512-row entries, a chunk after 300 cached keys, mixed prefill and decode), decode_extra R x 16
-    (DFlash's 1 + 15 rows; full and ragged) -- each with windows 0 and 128, and the drafter's
-    non-causal, sink-free call at the decode_extra shapes. Contexts come from random.Random(0) in
-    the reference's draw order, so the shapes are the reference's own; case i is drawn with
-    seed i, as the reference draws it."""
-    import random
-
-    rng = random.Random(0)
+def _reference_shapes(rng) -> list[tuple[str, dict]]:
+    """(label, Batch fields without window) over kelpie's build families (bench_attention.py:
+    62-84), contexts drawn from `rng` in the reference's draw order."""
     max_seq, k_extra, decode = 512, 15, (1, 2, 4, 8)
     shapes: list[tuple[str, dict]] = []
     for r in decode:
@@ -303,12 +293,43 @@ def reference_cases() -> list[tuple[str, Batch]]:
         shapes.append((f"decode_extra R={r}", dict(entries=full, tokens=r * w, reqs=r)))
         ragged = [(rng.randint(1, 600), 1 + rng.randint(0, k_extra)) for _ in range(r)]
         shapes.append((f"decode_extra R={r} ragged", dict(entries=ragged, tokens=r * w, reqs=r)))
+    return [(label, {**kw, "entries": tuple(tuple(e) for e in kw["entries"])})
+            for label, kw in shapes]
+
+
+def reference_cases() -> list[tuple[str, Batch]]:
+    """The shapes kelpie's per-op proof grades `paged_attention` on (kelpie/scripts/
+    bench_attention.py:42-91): gpt-oss-20b attention (64 q / 8 kv heads, D 64, block 16, sinks)
+    at the build's step families for max_seq_len 512, 8 requests, 1024 batch tokens -- decode
+    R = 1..8 (and 5 real entries padded to 8), prefill T = 1..1024 (fresh prompts split over
+    512-row entries, a chunk after 300 cached keys, mixed prefill and decode), decode_extra R x 16
+    (DFlash's 1 + 15 rows; full and ragged) -- each with windows 0 and 128, and the drafter's
+    non-causal, sink-free call at the decode_extra shapes. Contexts come from random.Random(0) in
+    the reference's draw order, so the shapes are the reference's own; case i is drawn with
+    seed i, as the reference draws it."""
+    import random
+
     cases = []
-    for label, kw in shapes:
-        kw = {**kw, "entries": tuple(tuple(e) for e in kw["entries"])}
+    for label, kw in _reference_shapes(random.Random(0)):
         for window in (0, 128):
             cases.append((f"{label} w{window}", Batch(**kw, window=window, **GPT_OSS_ATTN)))
         if label.startswith("decode_extra"):
             cases.append((f"{label} drafter", Batch(**kw, sinks=False, causal=False,
                                                     **GPT_OSS_ATTN)))
     return cases
+
+
+def reference_buckets() -> list[tuple[str, Batch, bool]]:
+    """The reference's timing buckets (bench_attention.py:211-237): its shapes drawn from
+    random.Random(1), without the chunked, mixed and 5-real cases, each at windows 0 and 128, as
+    (label, batch, graphed): decode-shaped steps are timed as graph replays, prefill eagerly."""
+    import random
+
+    out = []
+    for label, kw in _reference_shapes(random.Random(1)):
+        if "chunk" in label or "mixed" in label or "(5 real)" in label:
+            continue
+        for window in (0, 128):
+            out.append((f"{label} w{window}", Batch(**kw, window=window, **GPT_OSS_ATTN),
+                        not label.startswith("prefill")))
+    return out
