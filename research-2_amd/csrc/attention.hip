@@ -37,6 +37,7 @@
 #include <type_traits>
 
 #include "kvpath_device.h"
+#include "kvpath_fp8.h"
 #include "kvpath_internal.h"
 
 namespace kvpath {
@@ -512,6 +513,96 @@ __device__ __forceinline__ void append_rows_of_entry(const AttnArgs& a, const En
     }
 }
 
+// Fused fp8 append: this step's rows i in [i_lo, i_hi) of entry e (the entry's last n_rows
+// keys), for kv head h, under the quantize-on-append rule of kvpath_fp8.h, by the workgroup whose
+// partition holds them. Partitions start on 32-key boundaries and a page holds `block` keys with
+// 32 % block == 0, so every page these rows land in lies inside this partition: no other
+// workgroup of the launch reads its head-h bytes or scales, and this one reads them only after
+// the barrier that follows the call. (The rows' slots are their positions' slots in the entry's
+// table, as the engine's plans give them.) Each run of rows in one page becomes two units (K, V);
+// a group of D / 8 lanes takes a unit, a lane 8 dims. The first kRunKeep rows of a run stay in
+// registers between the absmax and the quantize pass (a decode entry's rows: n_rows * G <= 16,
+// so at most 4 rows when G >= 4); longer runs read theirs twice. Rows whose slot lies outside the
+// pool are skipped. The bytes and scales equal append_fp8_runs' (the clamped conversion it uses
+// for non-finite runs gives its unclamped one's result on finite ones).
+constexpr int kRunKeep = 4;
+
+template <int D, int NTH>
+__device__ __forceinline__ void append_fp8_rows_of_entry(const AttnArgs& a, const Entry& e, int h, int i_lo,
+                                                         int i_hi) {
+    constexpr int L = D / 8;
+    constexpr int kGroups = NTH / L;
+    const int n = i_hi - i_lo;
+    if (n <= 0) return;
+    const int64_t block = a.c.block, pool = a.c.num_pages * block;
+    const int lane = static_cast<int>(threadIdx.x) % L;
+    uint8_t* cache = static_cast<uint8_t*>(a.c.base);
+    for (int u = static_cast<int>(threadIdx.x) / L; u < 2 * n; u += kGroups) {
+        const int j = u >> 1, m = u & 1;
+        const int64_t t0 = e.q0 + i_lo + j;
+        const int64_t slot0 = a.slots[t0];
+        const int64_t page = page_of(slot0, block, pool);
+        if (page < 0) continue;
+        if (j > 0 && page_of(a.slots[t0 - 1], block, pool) == page) continue;  // not a run's first row
+        int len = 1;
+        uint64_t written = 1ull << (slot0 - page * block);
+        while (j + len < n) {
+            const int64_t s2 = a.slots[t0 + len];
+            if (page_of(s2, block, pool) != page) break;
+            written |= 1ull << (s2 - page * block);
+            ++len;
+        }
+        const bool fresh = written & 1ull;
+        const uint16_t* src = static_cast<const uint16_t*>(m ? a.v_new : a.k_new) +
+                              h * (m ? a.vn_shead : a.kn_shead) + 8 * lane;
+        const int64_t s_row = m ? a.vn_srow : a.kn_srow;
+        float* scale_slot = a.c.scale + (page * 2 + m) * a.c.hkv + h;
+        const float s_old = fresh ? 0.0f : *scale_slot;
+        u32x4 keep[kRunKeep];
+#pragma unroll
+        for (int r = 0; r < kRunKeep; ++r)
+            keep[r] = r < len ? *reinterpret_cast<const u32x4*>(src + (t0 + r) * s_row) : u32x4{0, 0, 0, 0};
+        float amax = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kRunKeep; ++r) {
+            float x[8];
+            widen_bf16x8(keep[r], x);
+            amax = fmaxf(amax, absmax8(x));
+        }
+        for (int r = kRunKeep; r < len; ++r) {
+            float x[8];
+            widen_bf16x8(*reinterpret_cast<const u32x4*>(src + (t0 + r) * s_row), x);
+            amax = fmaxf(amax, absmax8(x));
+        }
+#pragma unroll
+        for (int o = L / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, L));
+        int k;
+        const float s_new = grow_scale(s_old, __fdiv_rn(amax, kFp8Max), k);
+        const float r_new = s_new > 0.0f ? __fdiv_rn(1.0f, s_new) : 0.0f;
+        const int64_t head_base = page * a.c.s_page + m * a.c.s_kv + h * a.c.s_head + 8 * lane;
+        if (k > 0) {  // the page's other rows: an exponent shift
+            for (int64_t row = 0; row < block; ++row) {
+                if (written >> row & 1ull) continue;
+                u32x2* p = reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row);
+                *p = requant8(*p, k);
+            }
+        }
+        for (int r = 0; r < len; ++r) {
+            float x[8];
+            u32x4 w = keep[0];
+#pragma unroll
+            for (int q = 1; q < kRunKeep; ++q)
+                if (r == q) w = keep[q];
+            if (r >= kRunKeep) w = *reinterpret_cast<const u32x4*>(src + (t0 + r) * s_row);
+            widen_bf16x8(w, x);
+            const int64_t row = static_cast<int64_t>(a.slots[t0 + r]) - page * block;
+            *reinterpret_cast<u32x2*>(cache + head_base + row * a.c.s_row) =
+                r_new > 0.0f ? quantize8(x, r_new) : u32x2{0, 0};
+        }
+        if (lane == 0) *scale_slot = s_new;
+    }
+}
+
 // DIRECT: this launch writes `out` itself (one partition holds every row's keys) and its grid has
 // the z == R slice that zeroes dead rows; a separate instantiation, so the split-KV kernel carries
 // none of it.
@@ -585,6 +676,16 @@ __device__ __forceinline__ void partition_body(const AttnArgs& a, char* lds) {
     if (fused_append && tg0 == 0)
         append_rows_of_entry<D, kThreads>(a, e, h, max(0, part_lo - first_new),
                                           min(e.n_rows, part_hi - first_new));
+    // An fp8 cache's fused append quantizes into the pages this partition holds, and the
+    // attention below then reads them from the cache like every other key (after the barrier,
+    // which also orders the stores: workgroup scope suffices, every reader is in this workgroup).
+    if constexpr (FP8 && NT == 1) {
+        if (a.k_new != nullptr) {
+            append_fp8_rows_of_entry<D, kThreads>(a, e, h, max(0, part_lo - first_new),
+                                                  min(e.n_rows, part_hi - first_new));
+            __syncthreads();
+        }
+    }
     const char* k_new_head = fused_append ? static_cast<const char*>(a.k_new) +
                                                 static_cast<int64_t>(h) * a.kn_shead * 2 : nullptr;
     const char* v_new_head = fused_append ? static_cast<const char*>(a.v_new) +
@@ -1926,10 +2027,12 @@ void partition_shape(AttnArgs& a, int& nt, dim3& grid) {
 }
 
 bool attention_fuses(const AttnArgs& a) {
-    // Decode-shaped bf16 steps. (The multi-row kernel taking the append measured slower on
-    // DFlash verify: the new-key paths pushed it past the VGPRs of three waves per SIMD, and the
-    // spills cost more than the append launch saved.)
-    if (!mfma_serves(a) || a.c.dt != DT_BF16 || a.c.d % 8 != 0) return false;
+    // Decode-shaped steps, bf16 or fp8 cache. (The multi-row kernel taking the append measured
+    // slower on DFlash verify: the new-key paths pushed it past the VGPRs of three waves per SIMD,
+    // and the spills cost more than the append launch saved.) An fp8 cache needs every page
+    // inside one partition (32 % block == 0): its append rewrites whole pages' scales.
+    if (!mfma_serves(a) || a.c.d % 8 != 0) return false;
+    if (a.c.dt != DT_BF16 && !(a.c.dt == DT_FP8 && a.c.block > 0 && 32 % a.c.block == 0)) return false;
     AttnArgs b = a;
     int nt;
     dim3 grid;

@@ -204,10 +204,14 @@ int32_t append_impl(const kvpath::CacheView& c, const kvpath_rows* k, const kvpa
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Whether this step's append can run inside the attention kernel: bf16 rows into a bf16 cache,
-// 16-byte aligned, on the decode-shaped path.
+// Whether this step's append can run inside the attention kernel: bf16 rows, 16-byte aligned,
+// into a bf16 cache (16-byte chunks) or an fp8 one (8-byte e4m3 chunks), on the decode-shaped
+// path.
 bool append_fuses(const kvpath::AppendArgs& ap, const kvpath::AttnArgs& a) {
-    return a.c.dt == KVPATH_BF16 && ap.in_dt == KVPATH_BF16 && ap.T == a.T && aligned16(ap.k) &&
+    const bool cache_ok = a.c.dt == KVPATH_BF16 ||
+                          (a.c.dt == KVPATH_FP8_E4M3 && a.c.scale != nullptr &&
+                           (reinterpret_cast<uintptr_t>(a.c.base) & 7) == 0);
+    return cache_ok && ap.in_dt == KVPATH_BF16 && ap.T == a.T && aligned16(ap.k) &&
            aligned16(ap.v) && ap.k_srow % 8 == 0 && ap.k_shead % 8 == 0 && ap.v_srow % 8 == 0 &&
            ap.v_shead % 8 == 0 && (a.c.s_page % 8 == 0) && (a.c.s_row % 8 == 0) &&
            (a.c.s_kv % 8 == 0) && (a.c.s_head % 8 == 0) && kvpath::attention_fuses(a);
