@@ -223,15 +223,10 @@ def reference_buckets_line() -> dict:
         log(f"{label}: {us:.2f} us ({row['timing']})")
         del args
         torch.cuda.empty_cache()
-    # The same timing of one trivial kernel (a one-element add): the launch floor every bucket
-    # carries, graphed and eager.
-    one = torch.zeros(1, device="cuda")
-    floor = {"graph_us": round(time_call(lambda x: x.add_(1), (one,), True), 2),
-             "eager_us": round(time_call(lambda x: x.add_(1), (one,), False), 2)}
     return {"mode": "reference_buckets", "unit": "us per layer (gpt-oss attention: 64 q / 8 kv "
             "heads, D 64, block 16, sinks; append + attention, one op call)", "n_gpus": 1,
             "published": "kelpie/NOTES-attn.md:44-49 (A100/H100; context, not a target)",
-            "launch_floor": floor, "rows": rows}
+            "rows": rows}
 
 
 def measured_traffic(kernel: str, workload: str) -> int | None:
