@@ -181,31 +181,33 @@ def test_fp8_decode_stream(dim, rows_last) -> None:
     assert rms <= 1.25 * rms_fresh, (rms, rms_fresh)
 
 
-@pytest.mark.parametrize("dim,rows,window,sinks,partition", [
-    (128, 1, 0, False, 0),       # config 4's shape: the library's split
-    (128, 1, 0, False, 512),     # fixed 512-key partitions
-    (128, 3, 0, False, 0),       # three rows per entry: runs that cross a page boundary
-    (64, 1, 128, True, 0),       # gpt-oss's sliding layer: window, sinks, D 64
-    (256, 1, 0, False, 0),
-    (128, 1, 0, False, 8192),    # one partition per entry: the kernel writes `out` itself
+@pytest.mark.parametrize("dim,rows,window,sinks,partition,block", [
+    (128, 1, 0, False, 0, 16),       # config 4's shape: the library's split
+    (128, 1, 0, False, 512, 16),     # fixed 512-key partitions
+    (128, 3, 0, False, 0, 16),       # three rows per entry: runs that cross a page boundary
+    (64, 1, 128, True, 0, 16),       # gpt-oss's sliding layer: window, sinks, D 64
+    (256, 1, 0, False, 0, 16),
+    (128, 1, 0, False, 8192, 16),    # one partition per entry: the kernel writes `out` itself
+    (128, 3, 0, False, 0, 32),       # 32-token pages: a page is a whole 32-key block
 ])
 def test_fused_fp8_decode_append_equals_append_then_attend(dim, rows, window, sinks,
-                                                           partition) -> None:
+                                                           partition, block) -> None:
     """An fp8 decode step whose append runs inside the decode kernel (each page quantized by the
     one workgroup that reads it) leaves the bytes and scales kvpath.write_kv leaves and returns
     kvpath.attend's output over them, bit for bit: fresh pages, pages whose scale grows (a third
     of the step's rows scaled x30, so their pages' other rows are requantized), runs across a page
     boundary, pad rows (which only the unfused append writes, into the null page's scratch
     slot, so page 0 is left out)."""
-    say("fused fp8 decode append D", dim, "rows", rows, "window", window, "partition", partition)
+    say("fused fp8 decode append D", dim, "rows", rows, "window", window, "partition", partition,
+        "block", block)
     g = torch.Generator().manual_seed(dim * 10 + rows + window)
     ctx = [int(x) for x in torch.randint(1, 3000, (24,), generator=g)]
-    ctx[:4] = [0, 32, 15, 47]    # fresh pages; rows from a page's last slot on
+    ctx[:4] = [0, 2 * block, block - 1, 3 * block - 1]  # fresh pages; rows from a page's last slot
     heads = 64 if dim == 64 else 32
     n_rows = len(ctx) * rows
     batch = Batch(entries=tuple((n, rows) for n in ctx), tokens=n_rows + 5, reqs=len(ctx) + 1,
-                  heads=heads, kv_heads=8, head_dim=dim, block=16, window=window, sinks=sinks)
-    st = synthetic(batch, "cuda", torch.bfloat16, seed=dim + rows, pool_pages=6000,
+                  heads=heads, kv_heads=8, head_dim=dim, block=block, window=window, sinks=sinks)
+    st = synthetic(batch, "cuda", torch.bfloat16, seed=dim + rows, pool_pages=6000 * 16 // block,
                    cache_dtype=torch.float8_e4m3fn, outliers=0.01)
     args = list(st.args)
     q, k, v, member, rr, _, qsl, lens, table, slots, win, snk, causal = args
