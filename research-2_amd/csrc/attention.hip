@@ -376,6 +376,33 @@ __device__ __forceinline__ u32x2 lds_read_b64_async(uint32_t addr) {
     return v;
 }
 
+// ds_read_b128 / ds_read_b64_tr_b16, untracked like lds_read_b128_async / lds_read_tr16_async,
+// at a compile-time byte offset from the address register: a ring slot's offset goes into the
+// instruction's 16-bit offset field, so one address register serves every slot (a register
+// operand per slot and read would cost the multi-row kernels dozens of VGPRs).
+// (Offsets past the field's 16 bits, from D 256's larger slots, go into the address instead.)
+template <int Off>
+__device__ __forceinline__ u32x4 lds_read_b128_at(uint32_t addr) {
+    static_assert(Off >= 0, "LDS offsets are unsigned");
+    u32x4 v;
+    if constexpr (Off < 65536)
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(Off) : "memory");
+    else
+        v = lds_read_b128_async(addr + Off);
+    return v;
+}
+
+template <int Off>
+__device__ __forceinline__ v4s lds_read_tr16_at(uint32_t addr) {
+    static_assert(Off >= 0, "LDS offsets are unsigned");
+    v4s v;
+    if constexpr (Off < 65536)
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(Off) : "memory");
+    else
+        v = lds_read_tr16_async(addr + Off);
+    return v;
+}
+
 // ds_read_b64_tr_b8, untracked: lane 8a + b of each 16-lane group receives byte b of the 8-byte
 // rows addressed by lanes a, a + 2, ..., a + 14 of its group (probed on the GPU), so one read
 // gives a lane eight keys' bytes of one column.
@@ -1253,17 +1280,26 @@ void attn_partition_verify(AttnArgs a) {
                                            ((lane % CPK) ^ sw) * 16);
         ld_dst[bi] = static_cast<uint32_t>(member * L::kTile + (s * KK + j) * 1024);
     }
+    // LDS read addresses within a ring slot (the slot's offset is an immediate of each read).
     // K operand reads: lane (c, g) takes key 16s + c, chunk 4kk + g.
+    const uint32_t lds0 = lds_addr(lds);
     uint32_t k_rd[2][KK];
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
-            k_rd[s2][kk] = static_cast<uint32_t>((16 * s2 + c) * 2 * D + (((4 * kk + g) ^ k_swizzle<D>(c)) * 16));
-    const int r_row = 4 * g + (c >> 2);  // transposed-read source key (within a slice)
-    const uint32_t v_rd_row = static_cast<uint32_t>(L::kTile + r_row * 2 * D + (c & 1) * 8);
-    const int v_sw = v_swizzle<D>(r_row);
-    const uint32_t lds0 = lds_addr(lds);
+            k_rd[s2][kk] = lds0 + static_cast<uint32_t>((16 * s2 + c) * 2 * D + (((4 * kk + g) ^ k_swizzle<D>(c)) * 16));
+    // V operand reads (transposed): lane (c, g) reads key row 4g + c/4 of each slice, column
+    // block nb's chunk 2nb + (c & 3)/2 at its swizzled slot.
+    uint32_t v_rd[NB];
+    {
+        const int r_row = 4 * g + (c >> 2);
+        const int v_sw = v_swizzle<D>(r_row);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            v_rd[nb] = lds0 + static_cast<uint32_t>(r_row * 2 * D + (c & 1) * 8 +
+                                                    (((2 * nb + ((c & 3) >> 1)) ^ v_sw) * 16));
+    }
 
     for (int tg = tg0; tg * kWaves * TPW < n_tiles; tg += a.tile_groups) {
         const int qr0 = tg * kRowsWg;
@@ -1352,14 +1388,14 @@ void attn_partition_verify(AttnArgs a) {
                 }
             };
 
-            auto compute_stage = [&](int i, int slot) {
+            auto compute_stage = [&](int i, auto slot_c) {
                 const int kb = kb_first + chunk + i;
-                const uint32_t stage = lds0 + slot * L::kStage;
+                constexpr int kOff = decltype(slot_c)::value * L::kStage;
                 u32x4 kop[2][KK];
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-                    for (int kk = 0; kk < KK; ++kk) kop[s2][kk] = lds_read_b128_async(stage + k_rd[s2][kk]);
+                    for (int kk = 0; kk < KK; ++kk) kop[s2][kk] = lds_read_b128_at<kOff>(k_rd[s2][kk]);
                 wait_lds_ops();
                 float sc[TPW][2][4];
 #pragma unroll
@@ -1379,7 +1415,7 @@ void attn_partition_verify(AttnArgs a) {
 #pragma unroll
                     for (int t = 0; t < TPW; ++t)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) sc[t][s2][j] = acc_s[t][j] * a.score_scale_log2;
+                        for (int j = 0; j < 4; ++j) sc[t][s2][j] = acc_s[t][j];  // raw: scaled in exp2's fma
                 }
                 if (kb * 32 < full_lo || kb * 32 + 32 > full_hi) {
 #pragma unroll
@@ -1405,7 +1441,7 @@ void attn_partition_verify(AttnArgs a) {
                     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) mx = fmaxf(mx, sc[t][s2][j]);
-                    mx = rows_max(mx);
+                    mx = rows_max(mx) * a.score_scale_log2;  // scale > 0 keeps the max
                     if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kRescaleLog2)) {
                         const float m_new = fmaxf(m_run[t], mx);
                         const float alpha = m_new == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
@@ -1414,14 +1450,14 @@ void attn_partition_verify(AttnArgs a) {
                         for (int nb = 0; nb < NB; ++nb) acc[t][nb] *= alpha;
                         m_run[t] = m_new;
                     }
-                    const float m_use = m_run[t] == kNegInf ? 0.0f : m_run[t];
+                    const float neg_m = m_run[t] == kNegInf ? 0.0f : -m_run[t];
                     float pr[2][4];
                     float sum = 0.0f;
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            pr[s2][j] = __builtin_amdgcn_exp2f(sc[t][s2][j] - m_use);
+                            pr[s2][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][s2][j], a.score_scale_log2, neg_m));
                             sum += pr[s2][j];
                         }
                     l_run[t] += sum;
@@ -1437,10 +1473,8 @@ void attn_partition_verify(AttnArgs a) {
                     v4s lo_b[kBatch], hi_b[kBatch];
 #pragma unroll
                     for (int j = 0; j < kBatch; ++j) {
-                        const int q = 2 * (nb0 + j) + ((c & 3) >> 1);
-                        const uint32_t addr = stage + v_rd_row + ((q ^ v_sw) * 16);
-                        lo_b[j] = lds_read_tr16_async(addr);
-                        hi_b[j] = lds_read_tr16_async(addr + KK * 1024);
+                        lo_b[j] = lds_read_tr16_at<kOff + L::kTile>(v_rd[nb0 + j]);
+                        hi_b[j] = lds_read_tr16_at<kOff + L::kTile + KK * 1024>(v_rd[nb0 + j]);
                     }
                     wait_lds_ops();
 #pragma unroll
@@ -1468,31 +1502,35 @@ void attn_partition_verify(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < S - 1; ++i)
                 if (i < n_here) load_stage(i, i);
-            // Unrolled by S so every ring slot is a compile-time offset.
-            for (int i0 = 0; i0 < n_here; i0 += S) {
-#pragma unroll
-                for (int u = 0; u < S; ++u) {
-                    const int i = i0 + u;
-                    if (i >= n_here) break;
-                    if (i + S - 2 < n_here) wait_vmem<(S - 2) * kLoads>(); else wait_vmem<0>();
-                    __builtin_amdgcn_s_barrier();
-                    if (i + S - 1 < n_here) load_stage(i + S - 1, (u + S - 1) % S);
-                    const int kb = kb_first + chunk + i;
-                    if (kb * 32 + 32 > e.seq_len) {
-                        // V rows past the context may hold anything (NaN included): zero them so a
-                        // zero probability cannot turn into NaN. This is the workgroup's last
-                        // block, so nothing else is in flight; all threads share the rows, then
-                        // a barrier before anyone reads the tile.
-                        char* vt = lds + u * L::kStage + L::kTile;
-                        for (int idx = static_cast<int>(threadIdx.x); idx < 32 * CPK; idx += kThreads) {
-                            const int key = idx / CPK;
-                            if (kb * 32 + key >= e.seq_len)
-                                *reinterpret_cast<u32x4*>(vt + key * 2 * D + (idx % CPK) * 16) = u32x4{0, 0, 0, 0};
-                        }
-                        __syncthreads();
+            // One block per step, unrolled by S so every ring slot is a compile-time offset.
+            auto step = [&](auto u_c, int i) {
+                constexpr int u = decltype(u_c)::value;
+                if (i + S - 2 < n_here) wait_vmem<(S - 2) * kLoads>(); else wait_vmem<0>();
+                __builtin_amdgcn_s_barrier();
+                if (i + S - 1 < n_here) load_stage(i + S - 1, (u + S - 1) % S);
+                const int kb = kb_first + chunk + i;
+                if (kb * 32 + 32 > e.seq_len) {
+                    // V rows past the context may hold anything (NaN included): zero them so a
+                    // zero probability cannot turn into NaN. This is the workgroup's last
+                    // block, so nothing else is in flight; all threads share the rows, then
+                    // a barrier before anyone reads the tile.
+                    char* vt = lds + u * L::kStage + L::kTile;
+                    for (int idx = static_cast<int>(threadIdx.x); idx < 32 * CPK; idx += kThreads) {
+                        const int key = idx / CPK;
+                        if (kb * 32 + key >= e.seq_len)
+                            *reinterpret_cast<u32x4*>(vt + key * 2 * D + (idx % CPK) * 16) = u32x4{0, 0, 0, 0};
                     }
-                    if (has_tile) compute_stage(i, u);
+                    __syncthreads();
                 }
+                if (has_tile) compute_stage(i, u_c);
+            };
+            static_assert(S == 3, "the step loop below is unrolled by three");
+            for (int i0 = 0; i0 < n_here; i0 += S) {
+                step(std::integral_constant<int, 0>{}, i0);
+                if (i0 + 1 >= n_here) break;
+                step(std::integral_constant<int, 1>{}, i0 + 1);
+                if (i0 + 2 >= n_here) break;
+                step(std::integral_constant<int, 2>{}, i0 + 2);
             }
             wait_vmem_all();
             __builtin_amdgcn_s_barrier();  // the next chunk / tile group reuses the ring
