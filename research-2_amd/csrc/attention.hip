@@ -648,8 +648,8 @@ __device__ __forceinline__ void partition_body(const AttnArgs& a, char* lds) {
     // destination untouched until the explicit wait; under high register pressure (D 256, or
     // four row tiles per wave) it copies the destinations into AGPRs right after the load and
     // reuses them (read before the data lands; the late data then overwrites the reuse), so
-    // only one-tile instances at D <= 128 keep them. The CPU test suite scans the built ISA for
-    // such uses.
+    // only one-tile instances at D <= 128 keep them. The build scans the ISA for such uses and
+    // refuses to link the library when it finds one (kvpath.isa_scan).
     constexpr bool kAsyncK = D <= 128 && NT == 1;
     constexpr int kWaves = W;   // waves per workgroup
     constexpr int kThreads = 64 * W;
