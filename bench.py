@@ -3,8 +3,9 @@
 config 2 (Llama-3-8B-shape decode: batch 64, context U[1k, 4k] seeded, 32 q / 8 kv heads, D 128,
 block 16, bf16, a 32k-page pool): append 1 token per sequence at its slot, then split-KV paged
 attention (each sequence split by its own length, <= 512-key partitions at this shape) and the
-reduce. The default run also measures config 3 (DFlash verify) and config 4 (fp8 KV decode) in
-the same process (`also`), the KV append at a bandwidth-sized step (bf16, and fp8 whole pages).
+reduce. The default run also measures every other config at its full shape in the same process
+(`also`: configs 3-5 and workloads 6-9), the KV append at a bandwidth-sized step (bf16, and fp8
+whole pages) and config 5's copy_blocks.
 `--config N` measures BASELINE config N (1-5) or workload N (6-9: chunked prefill, gpt-oss full
 and sliding-window decode, the DFlash drafter) alone.
 
@@ -43,7 +44,7 @@ sys.path[:0] = [str(ROOT), str(ROOT / "research-2_amd"), str(ROOT / "tests")]
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, 2.5 PFLOP/s
 CONFIG = 2
-ALSO = (3, 4)  # measured beside the headline in the default run
+ALSO = (3, 4, 5, 6, 7, 8, 9)  # measured beside the headline in the default run
 ROTATE = 3
 APPEND_ROWS = 65536
 METRIC = "paged decode attn HBM GB/s (% peak) + tokens/s; KV append GB/s; 1 MI355X"
@@ -493,7 +494,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--config", type=int, default=None,
                     help="measure this config alone (default: config 2, the headline, with "
-                         "configs 3 and 4 beside it)")
+                         "every other config beside it)")
     ap.add_argument("--partition", type=int, default=0,
                     help="a fixed split-KV partition length in keys (0: the library's split of "
                          "each sequence by its own length)")
