@@ -10,6 +10,8 @@ exactly zero.
 
 from __future__ import annotations
 
+import dataclasses
+
 import pytest
 import torch
 
@@ -437,6 +439,36 @@ def test_config_attention(cfg) -> None:
     subset = {1: None, 2: [0, 1, 17, 40, 63], 3: [0, 5, 15], 4: [0, 64, 127], 5: [2],
               6: [0, 3], 7: [0, 31, 63], 8: [0, 31, 63], 9: [0, 7, 15]}[cfg]
     _check_against_oracle(out, args, subset, atol, rtol, step.kv_scale, f"config {cfg}")
+
+
+def test_config2_padded_to_its_bucket() -> None:
+    """BASELINE config 2 as kelpie pads a step to its bucket (c_api.zig:1085-1153): 61 real decode
+    entries padded to R = 64, three pad rows, through the whole op (the decode kernel with the
+    append fused in). Pad rows are exactly zero; the pool changes only at the real rows' slots
+    (and at most the scratch slot, page 0's last row, that pad rows target), holding their k/v
+    bit for bit; the real rows match the fp64 oracle."""
+    batch, extra = config_batch(2)
+    padded = dataclasses.replace(batch, entries=batch.entries[:61])
+    assert (padded.tokens, padded.reqs, padded.n_rows) == (64, 64, 61)
+    say("config 2 padded to its bucket")
+    step = synthetic(padded, "cuda", torch.bfloat16, seed=2, pool_pages=extra["pool_pages"])
+    q, k, v, member, rr, pos, qsl, lens, table, slot_map, window, sinks, causal = step.args
+    before = member.clone()
+    out = kvpath.paged_attention(*step.args)
+    torch.cuda.synchronize()
+    n, block = padded.n_rows, padded.block
+    assert torch.equal(out[n:].cpu(), torch.zeros_like(out[n:].cpu()))
+    changed = (member.view(torch.int16) != before.view(torch.int16)).flatten(3).any(3).any(1)
+    allowed = torch.zeros_like(changed)
+    real = slot_map[:n].long()
+    allowed.view(-1)[real] = True
+    allowed[0, block - 1] = True
+    assert not (changed & ~allowed).any()
+    pages, rows = real // block, real % block
+    assert torch.equal(member[pages, 0, rows].view(torch.int16), k[:n].view(torch.int16))
+    assert torch.equal(member[pages, 1, rows].view(torch.int16), v[:n].view(torch.int16))
+    del before
+    _check_against_oracle(out, step.args, [0, 30, 60], BF16_ATOL, BF16_RTOL, None, "config 2 padded")
 
 
 @pytest.mark.parametrize("dim,rows,window,sinks", [
