@@ -126,7 +126,7 @@ struct WorkspaceLayout {
     int64_t o_bytes, ml_offset, total;
 };
 
-// The split-KV workspace: f32-sized partials [T, H, slots, D], then (m, l) [T, H, slots, 2].
+// The split-KV workspace: f32-sized partials [slots, T, H, D], then (m, l) [slots, T, H, 2].
 // total is -1 when a size overflows int64 (the caller refuses the call). Takes T below 2^31 and
 // H, D below 2^16.
 WorkspaceLayout workspace_layout(int64_t T, int64_t H, int64_t D, int64_t slots) {

@@ -65,12 +65,12 @@ struct AttnArgs {
                              // only as many as one entry's window can reach, from its first
                              // visible key
     int32_t tile_groups;     // grid columns per partition (row tiles split across workgroups)
-    // Partial outputs [T, H, n_parts, D]: with a bf16 q (part_bf16), each partition's output
+    // Partial outputs [n_parts, T, H, D]: with a bf16 q (part_bf16), each partition's output
     // normalized by its own sum and rounded to bf16 (the format vLLM's paged_attention_v2 and
     // FlashInfer's split-KV decode keep); otherwise un-normalized f32. Either way part_ml holds
     // (running max in log2 units, sum of weights) in f32.
     void* part_o;
-    float* part_ml;          // [T, H, n_parts, 2]
+    float* part_ml;          // [n_parts, T, H, 2]
     int32_t part_bf16;
     void* out;
     int64_t out_srow, out_shead;
