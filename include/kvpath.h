@@ -217,10 +217,11 @@ int32_t kvpath_attend_reduce(const kvpath_rows* q, const kvpath_cache* cache,
 /*
  * The whole op (replaces paged_attention, kernels/ops/paged_attention.py:67-140): append k/v
  * at slot_mapping, then attend, on one stream. For a decode-shaped step of bf16 rows into a bf16
- * cache, or into an fp8 cache with 32 % block_size == 0, the append runs inside the attention
- * kernel with the same bytes, scales and output (pad rows are then not written to the scratch
- * slot, which nothing reads); that relies on each real row's slot_mapping being its position's
- * slot in its entry's block table, as the engine's plans give it.
+ * cache, or into an fp8 cache with 32 % block_size == 0, and for a verify- or drafter-sized step
+ * (a few row tiles per entry) of bf16 rows into a bf16 cache, the append runs inside the
+ * attention kernel with the same bytes, scales and output (pad rows are then not written to the
+ * scratch slot, which nothing reads); that relies on each real row's slot_mapping being its
+ * position's slot in its entry's block table, as the engine's plans give it.
  */
 int32_t kvpath_paged_attention(const kvpath_rows* q, const kvpath_rows* k, const kvpath_rows* v,
                                const kvpath_cache* cache, const kvpath_plan* plan,

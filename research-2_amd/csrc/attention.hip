@@ -1258,6 +1258,16 @@ void attn_partition_verify(AttnArgs a) {
     const int part_lo = part_start(e, p);
     if (part_lo >= e.seq_len) return;
     const int part_hi = min(part_lo + e.part, e.seq_len);
+    // Fused append (one tile group per partition): this step's rows are the entry's last n_rows
+    // keys; the workgroup whose partition holds a row writes its K and V for head h before
+    // anything is loaded, and the barrier orders those stores before the ring's loads of the same
+    // slots (workgroup scope suffices: no other workgroup reads this partition's keys).
+    if (a.k_new != nullptr) {
+        const int first_new = e.seq_len - e.n_rows;
+        append_rows_of_entry<D, 64 * W>(a, e, h, max(0, part_lo - first_new),
+                                        min(e.n_rows, part_hi - first_new));
+        __syncthreads();
+    }
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -2069,17 +2079,21 @@ void partition_shape(AttnArgs& a, int& nt, dim3& grid) {
 }
 
 bool attention_fuses(const AttnArgs& a) {
-    // Decode-shaped steps, bf16 or fp8 cache. (The multi-row kernel taking the append measured
-    // slower on DFlash verify: the new-key paths pushed it past the VGPRs of three waves per SIMD,
-    // and the spills cost more than the append launch saved.) An fp8 cache needs every page
-    // inside one partition (32 % block == 0): its append rewrites whole pages' scales.
+    // Decode-shaped steps, bf16 or fp8 cache, and bf16 multi-row steps of one workgroup per
+    // partition. An fp8 cache needs every page inside one partition (32 % block == 0): its
+    // append rewrites whole pages' scales. (An earlier multi-row form that read the new keys
+    // from k/v inside its block loop spilled past three waves per SIMD; the verify kernel writes
+    // them to the cache before its loop instead, which costs no registers there.)
     if (!mfma_serves(a) || a.c.d % 8 != 0) return false;
     if (a.c.dt != DT_BF16 && !(a.c.dt == DT_FP8 && a.c.block > 0 && 32 % a.c.block == 0)) return false;
     AttnArgs b = a;
     int nt;
     dim3 grid;
     partition_shape(b, nt, grid);
-    return nt == 1;
+    // Multi-row bf16 steps whose partitions each have one workgroup (verify, drafter): the verify
+    // kernel writes a partition's rows before reading its keys. (Prefill-sized steps spread a
+    // partition's rows over several workgroups, which would read the keys another one writes.)
+    return nt == 1 || (a.c.dt == DT_BF16 && nt != 8 && b.tile_groups == 1);
 }
 
 // Whether the partition kernel can write `out` itself: one partition holds every row's keys

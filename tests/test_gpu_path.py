@@ -933,24 +933,27 @@ def test_config5_copy_blocks_bit_exact() -> None:
     assert torch.equal(got.contiguous().view(torch.uint8), want.contiguous().view(torch.uint8))
 
 
-@pytest.mark.parametrize("rows,heads,dim,window,partition", [
-    (1, 32, 128, 0, 0),       # decode: the append runs inside the decode kernel
-    (16, 32, 128, 0, 0),      # verify-shaped: append launch, then the multi-row kernel
-    (7, 64, 64, 40, 0),       # multi-row, D 64, window
-    (300, 32, 128, 0, 0),     # prefill-shaped: two tiles per wave, several tile groups
-    (300, 32, 128, 0, 1 << 16),  # ... one partition: direct output with the append
+@pytest.mark.parametrize("rows,heads,dim,window,partition,causal", [
+    (1, 32, 128, 0, 0, True),       # decode: the append runs inside the decode kernel
+    (16, 32, 128, 0, 0, True),      # verify-shaped: inside the multi-row kernel, per partition
+    (16, 32, 128, 0, 0, False),     # the drafter's non-causal block
+    (16, 32, 128, 0, 1 << 16, True),  # ... one partition: direct output
+    (16, 32, 256, 0, 0, True),      # verify-shaped at D 256
+    (7, 64, 64, 40, 0, True),       # multi-row, D 64, window
+    (300, 32, 128, 0, 0, True),     # prefill-shaped: append launch, then two tiles per wave
+    (300, 32, 128, 0, 1 << 16, True),  # ... one partition: direct output with the append
 ])
-def test_fused_append_step(rows, heads, dim, window, partition) -> None:
-    """The whole op (append inside the decode kernel, or before the multi-row kernel): the pool
-    rows at slot_mapping hold k, v bit-exact, nothing else in the pool changes, pad rows are
-    exact zeros, and the output matches the fp64 oracle and the two-step path (write_kv, then
-    attend)."""
-    say("fused append", rows, heads, dim, window, partition)
+def test_fused_append_step(rows, heads, dim, window, partition, causal) -> None:
+    """The whole op (append inside the decode kernel or the verify kernel, or launched before the
+    prefill kernel): the pool rows at slot_mapping hold k, v bit-exact, nothing else in the pool
+    changes, pad rows are exact zeros, and the output matches the fp64 oracle and the two-step
+    path (write_kv, then attend)."""
+    say("fused append", rows, heads, dim, window, partition, causal)
     base, _ = config_batch(2)
     entries = tuple((n, rows) for n, _ in base.entries[:6]) + ((0, rows), (15, min(rows, 3)))
     n_rows = sum(r for _, r in entries)
     batch = Batch(entries=entries, tokens=n_rows + 4, reqs=len(entries) + 2, heads=heads,
-                  kv_heads=8, head_dim=dim, block=16, window=window, sinks=False)
+                  kv_heads=8, head_dim=dim, block=16, window=window, sinks=False, causal=causal)
     step = synthetic(batch, "cuda", torch.bfloat16, seed=21 + rows, pool_pages=8192)
     q, k, v, kv_member, rr, pos, qsl, lens, table, slots, window, sinks, causal = step.args
     before = compact_member(kv_member)
