@@ -1942,6 +1942,88 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce_few(AttnArgs a) {
     }
 }
 
+// Few partitions with bf16 partials and a bf16 output (every MFMA step): attn_reduce_few with
+// eight dims per thread, so 16-byte partial loads and output stores and half the threads.
+__global__ __launch_bounds__(kReduceThreads) void attn_reduce_few_bf16x8(AttnArgs a) {
+    const int D = a.c.d;
+    const int n_vec = D / 8;
+    const int heads_per_wg = kReduceThreads / n_vec;
+    const int t = blockIdx.x;
+    const int hq = blockIdx.y * heads_per_wg + static_cast<int>(threadIdx.x) / n_vec;
+    const int v = static_cast<int>(threadIdx.x) % n_vec;
+    if (hq >= a.H) return;
+    Entry e;
+    const bool live = row_live(a, t, e);
+    const int64_t out_base = static_cast<int64_t>(t) * a.out_srow + static_cast<int64_t>(hq) * a.out_shead + 8 * v;
+    f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float scale = 0.0f;  // a dead row, or no visible key: exact zeros
+    if (live) {
+        int lo, hi;
+        const int qrow = (t - e.q0) * a.G;
+        visible_span(a, e, qrow, qrow + 1, lo, hi);
+        hi = min(hi, e.seq_len);
+        split_entry(a, e);
+        const int p_lo = (lo - e.anchor) / e.part, n_p = (hi - 1 - e.anchor) / e.part - p_lo + 1;
+        // As attn_reduce_few: every load issued before one wait, slots past n_p re-reading slot
+        // p_lo and masked after.
+        const int n_all = min(a.n_parts, kFewParts);
+        u32x2 mlv[kFewParts];
+        u32x4 pv[kFewParts];
+#pragma unroll
+        for (int i = 0; i < kFewParts; ++i) {
+            mlv[i] = u32x2{0, 0};
+            pv[i] = u32x4{0, 0, 0, 0};
+            if (i >= n_all) break;
+            const int p = p_lo + (i < n_p ? i : 0);
+            mlv[i] = load_x2_async(reinterpret_cast<const char*>(part_ml_ptr(a, t, hq, p)));
+            pv[i] = load_x4_async(reinterpret_cast<const char*>(part_o_bf16(a, t, hq, p) + 8 * v));
+        }
+        wait_vmem_all();
+#pragma unroll
+        for (int i = 0; i < kFewParts; ++i) {
+            after_wait(mlv[i]);
+            after_wait(pv[i]);
+        }
+        float mv[kFewParts], lv[kFewParts];
+#pragma unroll
+        for (int i = 0; i < kFewParts; ++i) {
+            mv[i] = i < n_p ? __uint_as_float(mlv[i][0]) : kNegInf;
+            lv[i] = i < n_p ? __uint_as_float(mlv[i][1]) : 0.0f;
+        }
+        float m = kNegInf;
+#pragma unroll
+        for (int i = 0; i < kFewParts; ++i) m = fmaxf(m, mv[i]);
+        float l = 0.0f;
+        if (m != kNegInf) {
+#pragma unroll
+            for (int i = 0; i < kFewParts; ++i) {
+                const float w = mv[i] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(mv[i] - m);
+                // The same arithmetic as attn_reduce_few, element for element.
+                const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                const f32x4 x0 = i < n_p ? widen_partial<true>(u32x2{pv[i][0], pv[i][1]}) : zero;
+                const f32x4 x1 = i < n_p ? widen_partial<true>(u32x2{pv[i][2], pv[i][3]}) : zero;
+                const float f = w * partial_scale<true>(lv[i]);
+                o0 += x0 * f;
+                o1 += x1 * f;
+                l += lv[i] * w;
+            }
+        }
+        if (l > 0.0f) {
+            if (a.sinks != nullptr) {
+                const float sink = a.sinks[hq] * kLog2e;
+                const float top = fmaxf(m, sink);
+                const float f = __builtin_amdgcn_exp2f(m - top);
+                scale = f / (l * f + __builtin_amdgcn_exp2f(sink - top));
+            } else {
+                scale = 1.0f / l;
+            }
+        }
+    }
+    const f32x4 a0 = o0 * scale, a1 = o1 * scale;
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + out_base) =
+        u32x4{pack_bf16(a0[0], a0[1]), pack_bf16(a0[2], a0[3]), pack_bf16(a1[0], a1[1]), pack_bf16(a1[2], a1[3])};
+}
+
 template <int D, bool FP8>
 hipError_t launch_mfma(const AttnArgs& a, int nt, dim3 grid, hipStream_t s) {
     if (nt == 1) {
@@ -2137,7 +2219,12 @@ hipError_t launch_reduce(const AttnArgs& a, hipStream_t s) {
     const bool few = a.n_parts <= kFewParts && a.c.d % 4 == 0 && a.c.d / 4 <= kReduceThreads &&
                      (a.out_dt != DT_BF16 || (a.out_shead % 4 == 0 && a.out_srow % 4 == 0 &&
                                               (reinterpret_cast<uintptr_t>(a.out) & 7) == 0));
-    if (few) {
+    if (few && a.part_bf16 && a.out_dt == DT_BF16 && a.c.d % 8 == 0 && a.c.d / 8 <= kReduceThreads &&
+        a.out_shead % 8 == 0 && a.out_srow % 8 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+        const int heads_per_wg = kReduceThreads / (a.c.d / 8);
+        const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + heads_per_wg - 1) / heads_per_wg));
+        hipLaunchKernelGGL(attn_reduce_few_bf16x8, grid, dim3(kReduceThreads), 0, s, a);
+    } else if (few) {
         const int heads_per_wg = kReduceThreads / (a.c.d / 4);
         const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + heads_per_wg - 1) / heads_per_wg));
         if (a.part_bf16)
