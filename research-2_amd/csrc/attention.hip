@@ -487,6 +487,15 @@ __device__ __forceinline__ void wait_vmem() {
 
 __device__ __forceinline__ void wait_lds_ops() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Wait until at most N LDS operations of this wave are outstanding. LDS operations complete in
+// issue order (scalar memory loads, which share the counter, only make it wait longer), so this
+// waits for everything but the last N LDS operations issued.
+template <int N>
+__device__ __forceinline__ void wait_lds() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is four bits");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Direct output, grid slice z == R: every row that is not live gets exact zeros (what the reduce
 // writes for it). Threads test one row each; the workgroup then zeroes the dead rows it found
 // together, 8 bytes (four bf16) per store. `list` holds NTH + 1 ints of LDS (NTH threads).
@@ -1410,7 +1419,21 @@ void attn_partition_verify(AttnArgs a) {
                 for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                     for (int kk = 0; kk < KK; ++kk) kop[s2][kk] = lds_read_b128_at<kOff>(k_rd[s2][kk]);
-                wait_lds_ops();
+                // Two tiles per wave (the registers allow it): the block's V operand reads go out
+                // right behind K's and land while QK^T and the softmax run; the wait lets them stay
+                // outstanding. One tile per wave reads V in batches after the softmax.
+                constexpr bool kEarlyV = TPW == 2;
+                v4s vlo[kEarlyV ? NB : 1], vhi[kEarlyV ? NB : 1];
+                if constexpr (kEarlyV) {
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) {
+                        vlo[nb] = lds_read_tr16_at<kOff + L::kTile>(v_rd[nb]);
+                        vhi[nb] = lds_read_tr16_at<kOff + L::kTile + KK * 1024>(v_rd[nb]);
+                    }
+                    wait_lds<(2 * NB < 15 ? 2 * NB : 15)>();
+                } else {
+                    wait_lds_ops();
+                }
                 float sc[TPW][2][4];
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
@@ -1480,6 +1503,21 @@ void attn_partition_verify(AttnArgs a) {
                         pb[t][2 * s2] = pack_prob(pr[s2][0], pr[s2][1]);
                         pb[t][2 * s2 + 1] = pack_prob(pr[s2][2], pr[s2][3]);
                     }
+                }
+                if constexpr (kEarlyV) {
+                    wait_lds_ops();
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) {
+                        after_wait(vlo[nb]);
+                        after_wait(vhi[nb]);
+                        const u32x2 lo2 = __builtin_bit_cast(u32x2, vlo[nb]), hi2 = __builtin_bit_cast(u32x2, vhi[nb]);
+                        const u32x4 va = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+                        for (int t = 0; t < TPW; ++t)
+                            acc[t][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(bf16x8, va), __builtin_bit_cast(bf16x8, pb[t]), acc[t][nb], 0, 0, 0);
+                    }
+                    return;
                 }
                 constexpr int kBatch = NB < 4 ? NB : 4;
 #pragma unroll
