@@ -1360,12 +1360,19 @@ void attn_partition_verify(AttnArgs a) {
         }
         f32x4 acc[TPW][NB];
         float m_run[TPW], l_run[TPW];
+        // Two tiles per wave sum each row's probabilities on the matrix unit, which has room (the
+        // vector unit has less): one more PV MFMA per tile and block against an all-ones V block
+        // gives every lane of row c its sum over the block's keys, in place of eight adds a tile
+        // and the final cross-lane sum. (It sums the bf16 probabilities the PV MFMAs use.)
+        constexpr bool kSumMfma = TPW == 2;
+        f32x4 acc_l[kSumMfma ? TPW : 1];
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4{0, 0, 0, 0};
             m_run[t] = kNegInf;
             l_run[t] = 0.0f;
+            if constexpr (kSumMfma) acc_l[t] = f32x4{0, 0, 0, 0};
         }
 
         const int kb_first = lo / 32, kb_last = (hi - 1) / 32;
@@ -1482,7 +1489,10 @@ void attn_partition_verify(AttnArgs a) {
                     if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kRescaleLog2)) {
                         const float m_new = fmaxf(m_run[t], mx);
                         const float alpha = m_new == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
-                        l_run[t] *= alpha;
+                        if constexpr (kSumMfma)
+                            acc_l[t] *= alpha;
+                        else
+                            l_run[t] *= alpha;
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) acc[t][nb] *= alpha;
                         m_run[t] = m_new;
@@ -1497,12 +1507,20 @@ void attn_partition_verify(AttnArgs a) {
                             pr[s2][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][s2][j], a.score_scale_log2, neg_m));
                             sum += pr[s2][j];
                         }
-                    l_run[t] += sum;
+                    if constexpr (!kSumMfma) l_run[t] += sum;
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2) {
                         pb[t][2 * s2] = pack_prob(pr[s2][0], pr[s2][1]);
                         pb[t][2 * s2 + 1] = pack_prob(pr[s2][2], pr[s2][3]);
                     }
+                }
+                if constexpr (kSumMfma) {
+                    constexpr uint32_t kOnes = 0x3f803f80u;  // a bf16 pair of 1.0
+                    const u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+#pragma unroll
+                    for (int t = 0; t < TPW; ++t)
+                        acc_l[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, pb[t]), acc_l[t], 0, 0, 0);
                 }
                 if constexpr (kEarlyV) {
                     wait_lds_ops();
@@ -1591,7 +1609,11 @@ void attn_partition_verify(AttnArgs a) {
         // This wave's tile partials: lane (c, g) holds q-row tq0 + 16t + c, dims 16nb + 4g + i.
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
-            const float l = rows_sum(l_run[t]);
+            float l;
+            if constexpr (kSumMfma)
+                l = acc_l[t][0];
+            else
+                l = rows_sum(l_run[t]);
             const int qrow = tq0 + 16 * t + c;
             if (a.direct) {
                 // The reduce's arithmetic for a row with a single partition, in bf16.
