@@ -1366,11 +1366,15 @@ void attn_partition_verify(AttnArgs a) {
         // and the final cross-lane sum. (It sums the bf16 probabilities the PV MFMAs use.)
         constexpr bool kSumMfma = TPW == 2;
         f32x4 acc_l[kSumMfma ? TPW : 1];
+        // m_thr: the raw score (before the log2-unit scale) above which a row rescales.
+        float m_thr[TPW];
+        const float inv_scale = 1.0f / a.score_scale_log2;
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4{0, 0, 0, 0};
             m_run[t] = kNegInf;
+            m_thr[t] = kNegInf;
             l_run[t] = 0.0f;
             if constexpr (kSumMfma) acc_l[t] = f32x4{0, 0, 0, 0};
         }
@@ -1480,14 +1484,17 @@ void attn_partition_verify(AttnArgs a) {
                 u32x4 pb[TPW];
 #pragma unroll
                 for (int t = 0; t < TPW; ++t) {
+                    // This lane's raw maximum against the row's threshold: a row rescales when
+                    // its block maximum exceeds its running one by more than kRescaleLog2, i.e.
+                    // when one of its lanes' maxima does. Only then is the row maximum formed
+                    // (cross-lane), so most blocks skip it.
                     float mx = kNegInf;
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) mx = fmaxf(mx, sc[t][s2][j]);
-                    mx = rows_max(mx) * a.score_scale_log2;  // scale > 0 keeps the max
-                    if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kRescaleLog2)) {
-                        const float m_new = fmaxf(m_run[t], mx);
+                    if (__builtin_amdgcn_ballot_w64(mx > m_thr[t])) {
+                        const float m_new = fmaxf(m_run[t], rows_max(mx) * a.score_scale_log2);
                         const float alpha = m_new == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
                         if constexpr (kSumMfma)
                             acc_l[t] *= alpha;
@@ -1496,6 +1503,7 @@ void attn_partition_verify(AttnArgs a) {
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) acc[t][nb] *= alpha;
                         m_run[t] = m_new;
+                        m_thr[t] = (m_new + kRescaleLog2) * inv_scale;
                     }
                     const float neg_m = m_run[t] == kNegInf ? 0.0f : -m_run[t];
                     float pr[2][4];
