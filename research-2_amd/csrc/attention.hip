@@ -1368,6 +1368,7 @@ void attn_partition_verify(AttnArgs a) {
         f32x4 acc_l[kSumMfma ? TPW : 1];
         // m_thr: the raw score (before the log2-unit scale) above which a row rescales.
         float m_thr[TPW];
+        float neg_m[TPW];  // -m_run (0 while no key is visible): the exp argument's offset
         const float inv_scale = 1.0f / a.score_scale_log2;
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
@@ -1375,6 +1376,7 @@ void attn_partition_verify(AttnArgs a) {
             for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4{0, 0, 0, 0};
             m_run[t] = kNegInf;
             m_thr[t] = kNegInf;
+            neg_m[t] = 0.0f;
             l_run[t] = 0.0f;
             if constexpr (kSumMfma) acc_l[t] = f32x4{0, 0, 0, 0};
         }
@@ -1504,15 +1506,15 @@ void attn_partition_verify(AttnArgs a) {
                         for (int nb = 0; nb < NB; ++nb) acc[t][nb] *= alpha;
                         m_run[t] = m_new;
                         m_thr[t] = (m_new + kRescaleLog2) * inv_scale;
+                        neg_m[t] = m_new == kNegInf ? 0.0f : -m_new;
                     }
-                    const float neg_m = m_run[t] == kNegInf ? 0.0f : -m_run[t];
                     float pr[2][4];
                     float sum = 0.0f;
 #pragma unroll
                     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            pr[s2][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][s2][j], a.score_scale_log2, neg_m));
+                            pr[s2][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][s2][j], a.score_scale_log2, neg_m[t]));
                             sum += pr[s2][j];
                         }
                     if constexpr (!kSumMfma) l_run[t] += sum;
