@@ -2106,7 +2106,8 @@ hipError_t launch_mfma(const AttnArgs& a, int nt, dim3 grid, hipStream_t s) {
     } else if constexpr (!FP8) {
         // Multi-row bf16 steps: the verify kernel (K/V staged once per workgroup), four waves of
         // one row tile, or of two for prefill-sized steps (nt 8, D <= 128). (Two waves of two
-        // tiles for verify-sized steps measured 3% slower on DFlash verify than four of one.)
+        // tiles for verify-sized steps measured 3% slower on DFlash verify than four of one, and
+        // still 1.5% slower with the two-tile kernel's early V reads and MFMA row sums.)
         if constexpr (D <= 128) {
             if (nt == 8) {
                 hipLaunchKernelGGL((attn_partition_verify<D, 2, 4>), grid, dim3(256), 0, s, a);
