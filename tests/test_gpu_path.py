@@ -417,11 +417,11 @@ def _check_against_oracle(out: torch.Tensor, args_gpu: tuple, entries: list[int]
     return ratio
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 def test_config_attention(cfg) -> None:
-    """Each BASELINE configuration (1-5), and each workload of the callers next to the path
+    """Each BASELINE configuration (1-5), each workload of the callers next to the path
     (6 chunked prefill, 7/8 gpt-oss full and sliding-window decode with sinks, 9 the DFlash
-    drafter's non-causal block), at its real shape (pool, heads, context lengths) through the
+    drafter's non-causal block), and config 2 at 4096 keys (10), at its real shape (pool, heads, context lengths) through the
     whole op, checked against the fp64 oracle on a subset of its entries."""
     batch, extra = config_batch(cfg)
     say("config", cfg, "entries", len(batch.entries))
@@ -437,7 +437,7 @@ def test_config_attention(cfg) -> None:
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     subset = {1: None, 2: [0, 1, 17, 40, 63], 3: [0, 5, 15], 4: [0, 64, 127], 5: [2],
-              6: [0, 3], 7: [0, 31, 63], 8: [0, 31, 63], 9: [0, 7, 15]}[cfg]
+              6: [0, 3], 7: [0, 31, 63], 8: [0, 31, 63], 9: [0, 7, 15], 10: [0, 31, 63]}[cfg]
     _check_against_oracle(out, args, subset, atol, rtol, step.kv_scale, f"config {cfg}")
 
 

@@ -192,11 +192,14 @@ CONFIG_NAMES = {
     7: "gpt_oss_full_decode_bf16",
     8: "gpt_oss_sliding_decode_bf16",
     9: "dflash_drafter_bf16",
+    # north_star's own wording of the decode target ("batch 64, ctx 4k"): config 2 at 4096 keys.
+    10: "llama3_8b_decode_ctx4k_bf16",
 }
 
 
 def config_batch(cfg: int, seed: int = 0) -> tuple[Batch, dict]:
-    """BASELINE.json's configs 1-5, and workloads 6-9 of the callers next to the path, as
+    """BASELINE.json's configs 1-5, workloads 6-9 of the callers next to the path, and workload
+    10 (config 2 with every context at 4096 keys, the decode target's stated shape), as
     (Batch, extras): pool size, dtypes, outliers. Context lengths are drawn from
     `seed` (a CPU generator) as the configs state."""
     g = torch.Generator(device="cpu").manual_seed(1000 + seed)
@@ -246,6 +249,11 @@ def config_batch(cfg: int, seed: int = 0) -> tuple[Batch, dict]:
         ctx = uniform(16, 512, 8192)
         b = Batch(entries=tuple((n, 16) for n in ctx), tokens=256, reqs=16, causal=False,
                   **{**llama, "sinks": False})
+        return b, dict(pool_pages=32768, dtype=torch.bfloat16)
+    if cfg == 10:
+        # The decode target as north_star words it: batch 64, ctx 4k (4095 cached keys and the
+        # appended one), config 2's heads, pages and pool.
+        b = Batch(entries=tuple((4095, 1) for _ in range(64)), tokens=64, reqs=64, **llama)
         return b, dict(pool_pages=32768, dtype=torch.bfloat16)
     raise ValueError(f"no config {cfg}")
 
