@@ -248,17 +248,10 @@ __device__ __forceinline__ void store_partial4(const AttnArgs& a, int t, int hq,
 
 // Dims [d, d + 4) of a partial as stored: four bf16 (8 bytes) or four f32. widen_partial turns
 // them into f32; times partial_scale<BF16P>(l) that is the partition's un-normalized output.
-// (Loads and widening are apart so a batch of predicated loads is issued before any wait.)
+// (The reduce kernels load them with untracked loads and widen them after one wait, so a batch
+// of loads is issued before any wait.)
 template <bool BF16P>
 using PartialRaw = std::conditional_t<BF16P, u32x2, f32x4>;
-
-template <bool BF16P>
-__device__ __forceinline__ PartialRaw<BF16P> load_partial4(const AttnArgs& a, int t, int hq, int p, int d) {
-    if constexpr (BF16P)
-        return *reinterpret_cast<const u32x2*>(part_o_bf16(a, t, hq, p) + d);
-    else
-        return *reinterpret_cast<const f32x4*>(part_o_f32(a, t, hq, p) + d);
-}
 
 template <bool BF16P>
 __device__ __forceinline__ f32x4 widen_partial(PartialRaw<BF16P> w) {

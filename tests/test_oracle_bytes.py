@@ -58,6 +58,21 @@ def test_e4m3_random_f32_and_decode() -> None:
     assert torch.equal(got[~nan], want[~nan])
 
 
+def test_fp8_quantize_is_the_clamped_scaled_cast() -> None:
+    """One value against a page scale through its reciprocal: x * r in f32, clamped to +-448,
+    then torch's e4m3 cast; 0 when the reciprocal is 0 (an all-zero page). Values reach past
+    the clamp on both sides, and a reciprocal that is not a power of two rounds the product."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4000, generator=g) * torch.exp(torch.randn(4000, generator=g) * 2)
+    for r in (0.0, 1.0, 3.0, 448.0 / 3.7, 2.0 ** -9, 1.0 / 0.0175):
+        rr = torch.tensor(r, dtype=torch.float32)
+        want = (x * rr).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        if r == 0.0:
+            want = torch.zeros_like(want)
+        got = torch.tensor([kvbytes.fp8_quantize(v, float(rr)) for v in x.tolist()], dtype=torch.uint8)
+        assert torch.equal(got, want), r
+
+
 # ---- append / gather / copy_blocks ----------------------------------------------------------------
 
 
