@@ -167,12 +167,15 @@ PUBLISHED_US = {
 }
 CASE_REPLAYS = 50
 CASE_WARMUP = 5
+CASE_LAYERS = 24  # gpt-oss-20b's attention layers
 
 
-def time_call(fn, args: tuple, graphed: bool) -> float:
+def time_call(fn, args: tuple, graphed: bool, calls: int = 1) -> float:
     """Median microseconds of one call over CASE_REPLAYS, as the reference times its buckets
     (bench_attention.py:189-208): one call captured in a hipGraph and replayed, HIP events around
-    each replay; or, eagerly, HIP events around each call."""
+    each replay; or, eagerly, HIP events around each call. With `calls` > 1 (graphed only) the
+    graph holds that many back-to-back calls, as a captured model step holds one per layer, and
+    each replay's time is divided by it."""
     import torch
 
     fn(*args)
@@ -182,7 +185,8 @@ def time_call(fn, args: tuple, graphed: bool) -> float:
         stream.wait_stream(torch.cuda.current_stream())
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
-            fn(*args)
+            for _ in range(calls):
+                fn(*args)
         torch.cuda.current_stream().wait_stream(stream)
         run = graph.replay
     else:
@@ -197,7 +201,7 @@ def time_call(fn, args: tuple, graphed: bool) -> float:
         run()
         end.record()
         end.synchronize()
-        times.append(start.elapsed_time(end) * 1e3)
+        times.append(start.elapsed_time(end) * 1e3 / calls)
     return statistics.median(times)
 
 
@@ -219,14 +223,21 @@ def reference_buckets_line() -> dict:
         us = time_call(kvpath.paged_attention, args, graphed)
         row = {"bucket": label, "us_per_layer": round(us, 2), "timing": "graph" if graphed else "eager",
                "rows": batch.n_rows, "tokens": batch.tokens}
+        if graphed:
+            # The same call once per layer of a captured step (gpt-oss-20b's 24 layers, no other
+            # ops between them): the per-layer cost without a graph launch per call.
+            row["us_per_layer_in_step"] = round(time_call(kvpath.paged_attention, args, True,
+                                                          CASE_LAYERS), 2)
         if label in PUBLISHED_US:
             row["published_us"] = PUBLISHED_US[label]
         rows.append(row)
-        log(f"{label}: {us:.2f} us ({row['timing']})")
+        log(f"{label}: {us:.2f} us ({row['timing']})"
+            + (f", {row['us_per_layer_in_step']:.2f} us in a {CASE_LAYERS}-layer graph" if graphed else ""))
         del args
         torch.cuda.empty_cache()
     return {"mode": "reference_buckets", "unit": "us per layer (gpt-oss attention: 64 q / 8 kv "
-            "heads, D 64, block 16, sinks; append + attention, one op call)", "n_gpus": 1,
+            "heads, D 64, block 16, sinks; append + attention, one op call; us_per_layer_in_step: "
+            f"one call per layer of a {CASE_LAYERS}-call graph)", "n_gpus": 1,
             "published": "kelpie/NOTES-attn.md:44-49 (A100/H100; context, not a target)",
             "rows": rows}
 
