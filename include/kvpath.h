@@ -156,7 +156,9 @@ int32_t kvpath_copy_blocks(const kvpath_cache* cache, const int32_t* src, const 
  * key rounded down to 32) are cut on the device, from its own seq_len, into
  * min(slots, ceil(span / partition_tokens)) partitions of equal length rounded up to 32 keys, so
  * the split does not depend on how wide the block table is beyond the slots an entry could fill
- * (kelpie sizes tables for max_seq_len).  With partition_tokens > 0 (a multiple of 32) every
+ * (kelpie sizes tables for max_seq_len).  A decode step over a table of at most 768 keys gets
+ * one slot: one partition per entry, written to `out` with no reduce.  With partition_tokens > 0
+ * (a multiple of 32) every
  * partition has that length and slots = ceil(table_width * block / partition_tokens).
  */
 typedef struct kvpath_split {

@@ -2191,11 +2191,18 @@ SplitChoice choose_split(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int6
     //  - prefill-sized steps (8+ workgroups per partition from their rows alone) fill the grid
     //    with rows: slots only up to 1024 workgroups (4 x 512-row chunks after 2k keys: one
     //    partition, 124 us, against 155-176 us split).
+    //  - decode over a table of at most 768 keys: one slot, so each entry is one partition and
+    //    the kernel writes `out` with no reduce launch. Per layer of a 24-call graph: gpt-oss
+    //    decode of 2-8 entries over <= 700 keys 7.0-8.6 us against 10.8-12.5 split; Llama-3-8B
+    //    decode at 512 keys 9.5-16.4 us against 12.4-24.9 for 1-32 entries. At 1024 keys the
+    //    split still wins up to 8 entries (13.7-19.4 against 12.4-16.4 us).
     // An odd slot count keeps the grid's x extent odd, which spreads each entry's partitions
     // over consecutive XCDs (part_slot).
     const int64_t wgs = n_reqs * kv_heads * groups;
     const bool prefill = groups >= 8;
     const bool multi_row = tiles > 1;
+    constexpr int64_t kOnePartitionKeys = 768;
+    if (!multi_row && keys <= kOnePartitionKeys) return SplitChoice{kBase, 1, 0};
     const int64_t base = prefill ? 512 : (multi_row ? 896 : kBase);
     int64_t cap = prefill ? std::max<int64_t>(1, 1024 / wgs)
                           : std::max<int64_t>(9, cdiv(multi_row ? 1024 : 2048, wgs));

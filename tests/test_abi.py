@@ -86,6 +86,9 @@ def _cache(**kw) -> _lib.Cache:
     ((2048, 4, 32, 8, 160, 16, 0), (512, 1, 1)),     # prefill, 512-row chunks after 2k keys
     ((8192, 1, 32, 8, 2048, 16, 0), (512, 3, 1)),    # one long prefill chunk: 1024 workgroups
     ((64, 64, 32, 8, 3, 16, 0), (512, 1, 1)),        # a table of 48 keys: one slot
+    ((64, 64, 32, 8, 34, 16, 0), (512, 1, 1)),       # decode over 544 keys: one partition each
+    ((8, 8, 64, 8, 45, 16, 0), (512, 1, 1)),         # gpt-oss decode over 720 keys: the same
+    ((8, 8, 32, 8, 64, 16, 0), (512, 2, 1)),         # decode over 1024 keys: split again
     ((0, 0, 32, 8, 1, 16, 0), (512, 1, 1)),          # empty step
     ((4, 4, 64, 8, 8192, 16, 512), (512, 256, 0)),   # a fixed 512: 256 partitions of 128k
     ((64, 64, 32, 8, 258, 16, 480), (480, 9, 0)),    # a fixed 480 over 4128 keys
@@ -94,7 +97,8 @@ def test_split_choice(lib, shape, want) -> None:
     """The library's split-KV plan. With partition 0, each entry is cut on the device by its own
     length: a floor of 512 keys (896 for verify-shaped steps), at most `slots` partitions per
     entry, where the slots give the grid 2048+ workgroups (decode) or 1024+ (verify), at least
-    nine, an odd count, and never more than the table could fill at the floor; prefill-sized
+    nine, an odd count, and never more than the table could fill at the floor; a decode step
+    over at most 768 keys takes one slot (one partition per entry, no reduce); prefill-sized
     steps fill the grid with rows and take slots only up to 1024 workgroups. A fixed partition
     length gives ceil(keys / length) slots."""
     T, R, H, hkv, width, block, part = shape
@@ -244,7 +248,8 @@ def test_newest_positions_assert() -> None:
 def test_split_choice_properties(lib) -> None:
     """Over a seeded sweep of step shapes: the floor length is a multiple of 32 of at least 512
     keys; the slots are at least one, no more than the table could fill at the floor, and do not
-    grow with the table's width once it exceeds that (kelpie pads tables to max_seq_len); the
+    grow with the table's width once it exceeds that (kelpie pads tables to max_seq_len), but for
+    a table of at most 768 keys, where a decode step takes one slot; the
     workspace is exactly the slots' partials."""
     g = torch.Generator().manual_seed(5)
     out = _lib.Split()
@@ -261,7 +266,9 @@ def test_split_choice_properties(lib) -> None:
         assert out.per_entry == 1 and part % 32 == 0 and part >= 512, shape
         assert 1 <= slots <= max(1, -(-width * block // part)), shape
         assert lib.kvpath_split_plan(T, R, H, hkv, width * 64, block, 0, ctypes.byref(out)) == 0
-        assert out.slots >= slots and (slots == -(-width * block // part) or out.slots == slots)
+        # (A step over at most 768 keys may take one slot: decode's one partition per entry.)
+        assert out.slots >= slots and (slots == -(-width * block // part) or out.slots == slots
+                                       or (slots == 1 and width * block <= 768))
         for dim in (64, 128):
             rows = T * H * slots
             want = (rows * dim * 4 + 255) // 256 * 256 + rows * 8
