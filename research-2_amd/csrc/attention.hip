@@ -2252,10 +2252,15 @@ bool attention_fuses(const AttnArgs& a) {
     int nt;
     dim3 grid;
     partition_shape(b, nt, grid);
-    // Multi-row bf16 steps whose partitions each have one workgroup (verify, drafter): the verify
-    // kernel writes a partition's rows before reading its keys. (Prefill-sized steps spread a
-    // partition's rows over several workgroups, which would read the keys another one writes.)
-    return nt == 1 || (a.c.dt == DT_BF16 && nt != 8 && b.tile_groups == 1);
+    // Multi-row bf16 steps of at most four workgroups per partition (verify, drafter; gpt-oss's
+    // 1 + 15 rows x 8 q heads take two): each of the partition's workgroups writes the
+    // partition's new rows before reading its keys. Another workgroup of the partition may be
+    // writing the same slots meanwhile, but with the same bytes, and a workgroup's own stores
+    // are complete before its loads (its barrier), so every read sees the new row. Timed per
+    // layer in a 24-call graph, gpt-oss decode_extra (1-8 entries of 16 rows) went from
+    // 8.7-18.3 us with the append launch to 6.7-15.9. (Prefill-sized steps spread a
+    // partition's rows over 8+ workgroups: the copies would cost more than the launch.)
+    return nt == 1 || (a.c.dt == DT_BF16 && nt != 8 && b.tile_groups <= 4);
 }
 
 // Whether the partition kernel can write `out` itself: one partition holds every row's keys

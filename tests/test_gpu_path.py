@@ -940,6 +940,10 @@ def test_config5_copy_blocks_bit_exact() -> None:
     (16, 32, 128, 0, 1 << 16, True),  # ... one partition: direct output
     (16, 32, 256, 0, 0, True),      # verify-shaped at D 256
     (7, 64, 64, 40, 0, True),       # multi-row, D 64, window
+    (16, 64, 64, 0, 0, True),       # gpt-oss 1 + 15 rows: two workgroups per partition
+    (16, 64, 64, 128, 0, True),     # ... with its sliding window
+    (16, 64, 64, 0, 0, False),      # ... the drafter's non-causal block
+    (24, 64, 64, 0, 1 << 16, True),  # three workgroups, one partition: direct output
     (300, 32, 128, 0, 0, True),     # prefill-shaped: append launch, then two tiles per wave
     (300, 32, 128, 0, 1 << 16, True),  # ... one partition: direct output with the append
 ])
