@@ -441,6 +441,39 @@ def test_config_attention(cfg) -> None:
     _check_against_oracle(out, args, subset, atol, rtol, step.kv_scale, f"config {cfg}")
 
 
+@pytest.mark.parametrize("n,heads,dim,cache", [
+    (1, 32, 128, torch.bfloat16),
+    (8, 64, 64, torch.bfloat16),      # gpt-oss: 64 q / 8 kv heads, D 64, sinks
+    (32, 32, 128, torch.bfloat16),
+    (16, 32, 128, torch.float8_e4m3fn),
+])
+def test_short_decode_tables_take_one_partition(n, heads, dim, cache) -> None:
+    """A decode step over a table of at most 768 keys takes one slot: each entry is one
+    partition, written to `out` with no reduce. Its output meets the oracle's tolerance and
+    agrees with the same step forced through split-KV partitions of 128 keys and the reduce
+    (fp32 rounding apart); pad rows stay zero."""
+    say("short decode table", n, heads, dim, cache)
+    ctx = [int(x) for x in torch.randint(1, 720, (n,), generator=torch.Generator().manual_seed(n))]
+    batch = Batch(entries=tuple((c, 1) for c in ctx), tokens=n + 2, reqs=n + 1, heads=heads,
+                  kv_heads=8, head_dim=dim, block=16, sinks=heads == 64)
+    step = synthetic(batch, "cuda", torch.bfloat16, seed=60 + n, pool_pages=4096,
+                     cache_dtype=None if cache == torch.bfloat16 else cache)
+    width = step.args[8].shape[1]
+    assert width * 16 <= 768
+    assert kvpath.split_plan(batch.tokens, batch.reqs, heads, 8, width, 16, 0)[1] == 1
+    fp8 = step.kv_scale is not None
+    run = ((lambda **kw: kvpath.paged_attention_fp8(*step.args, step.kv_scale, **kw)) if fp8
+           else (lambda **kw: kvpath.paged_attention(*step.args, **kw)))
+    one = run()
+    split = run(partition=128)
+    torch.cuda.synchronize()
+    assert torch.equal(one[batch.n_rows:].cpu(), torch.zeros_like(one[batch.n_rows:].cpu()))
+    atol, rtol = (FP8_ATOL, FP8_RTOL) if fp8 else (BF16_ATOL, BF16_RTOL)
+    ok, ratio = within(one.cpu().float(), split.cpu().float(), atol, rtol)
+    assert ok, ratio
+    _check_against_oracle(one, step.args, None, atol, rtol, step.kv_scale, label="one partition")
+
+
 def test_config2_padded_to_its_bucket() -> None:
     """BASELINE config 2 as kelpie pads a step to its bucket (c_api.zig:1085-1153): 61 real decode
     entries padded to R = 64, three pad rows, through the whole op (the decode kernel with the
