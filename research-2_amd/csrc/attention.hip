@@ -1269,10 +1269,11 @@ void attn_partition_verify(AttnArgs a) {
     const int part_lo = part_start(e, p);
     if (part_lo >= e.seq_len) return;
     const int part_hi = min(part_lo + e.part, e.seq_len);
-    // Fused append (one tile group per partition): this step's rows are the entry's last n_rows
-    // keys; the workgroup whose partition holds a row writes its K and V for head h before
-    // anything is loaded, and the barrier orders those stores before the ring's loads of the same
-    // slots (workgroup scope suffices: no other workgroup reads this partition's keys).
+    // Fused append (at most four tile groups per partition): this step's rows are the entry's
+    // last n_rows keys; every workgroup whose partition holds a row writes its K and V for head h
+    // before anything is loaded, and the barrier orders its own stores before its ring's loads of
+    // the same slots. The partition's other tile groups write the same bytes to the same slots,
+    // so whichever store a load sees, it reads the new row.
     if (a.k_new != nullptr) {
         const int first_new = e.seq_len - e.n_rows;
         append_rows_of_entry<D, 64 * W>(a, e, h, max(0, part_lo - first_new),
