@@ -208,19 +208,18 @@ def time_call(fn, args: tuple, graphed: bool, calls: int = 1) -> float:
 
 def reference_buckets_line() -> dict:
     """Microseconds per layer for the reference's timing buckets (workloads.reference_buckets),
-    each drawn by the reference's generator with seed 20 as it draws them, the published A100 /
-    H100 figures beside the six buckets kelpie/NOTES-attn.md lists."""
+    each drawn on the device by workloads.synthetic with seed 20, the published A100 / H100
+    figures beside the six buckets kelpie/NOTES-attn.md lists."""
     import torch
 
     import kvpath
     from kvpath import _lib
-    from reference_sample import sample
-    from workloads import reference_buckets
+    from workloads import reference_buckets, synthetic
 
     _lib.load()  # fails loudly without the HIP library
     rows = []
     for label, batch, graphed in reference_buckets():
-        args = sample(batch, "cuda", torch.bfloat16, seed=20)
+        args = synthetic(batch, "cuda", torch.bfloat16, seed=20).args
         us = time_call(kvpath.paged_attention, args, graphed)
         row = {"bucket": label, "us_per_layer": round(us, 2), "timing": "graph" if graphed else "eager",
                "rows": batch.n_rows, "tokens": batch.tokens}

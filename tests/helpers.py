@@ -1,4 +1,4 @@
-"""Shared test helpers: golden-case batches, digests, the grading rule."""
+"""Shared test helpers: golden-case batches and inputs, digests, the grading rule."""
 
 from __future__ import annotations
 
@@ -6,8 +6,10 @@ import hashlib
 
 import torch
 
-from reference_sample import SAMPLE_BATCH
-from workloads import Batch
+from kvpath.paged_attention import KV_MEMBERS
+from workloads import GARBAGE, Batch
+
+PLAN = ("row_request", "positions", "query_start_loc", "seq_lens", "block_table", "slot_mapping")
 
 
 def batch_of(meta_batch: dict) -> Batch:
@@ -17,7 +19,29 @@ def batch_of(meta_batch: dict) -> Batch:
 
 
 def golden_batch(name: str, meta: dict) -> Batch:
-    return SAMPLE_BATCH if name == "sample_batch" else batch_of(meta[name]["batch"])
+    return batch_of(meta[name]["batch"])
+
+
+def golden_args(name: str, golden: tuple[dict, dict], device: str | torch.device,
+                dtype: torch.dtype) -> tuple:
+    """The op's 13 arguments for golden case `name`, rebuilt from the fixture's bf16 draw: the
+    arena [pages, block, 2 members, K/V, Hkv, D] is GARBAGE with this layer (member 1) holding
+    the stored values, so the kv_member is a strided view as the reference's sample() lays it
+    out; fp32 and fp64 cases are exact upcasts of the bf16 values (sinks stay f32)."""
+    meta, arrays = golden
+    b = golden_batch(name, meta)
+
+    def stored(key: str) -> torch.Tensor:
+        return torch.from_numpy(arrays[f"{name}/in_{key}"].copy())
+
+    member = stored("member").view(torch.bfloat16).to(dtype)
+    arena = torch.full((member.shape[0], b.block, 2, KV_MEMBERS, b.kv_heads, b.head_dim), GARBAGE,
+                       dtype=dtype, device=device)
+    kv_member = arena[:, :, 1].permute(0, 2, 1, 3, 4)
+    kv_member.copy_(member.to(device))
+    q, k, v = (stored(x).view(torch.bfloat16).to(device=device, dtype=dtype) for x in "qkv")
+    plan = [stored(key).to(device) for key in PLAN]
+    return (q, k, v, kv_member, *plan, b.window, stored("sinks").to(device), b.causal)
 
 
 def digest(t: torch.Tensor) -> str:

@@ -213,11 +213,10 @@ def test_unsupported_is_not_implemented(lib) -> None:
 
 def test_python_layer_refuses_cpu_tensors() -> None:
     """There is no CPU path: CPU tensors raise instead of computing."""
-    from reference_sample import sample
-    from workloads import Batch
+    from workloads import Batch, step_args
 
-    args = sample(Batch(entries=((3, 1),), tokens=1, reqs=1, heads=4, kv_heads=2, head_dim=32,
-                        block=4), "cpu", torch.bfloat16)
+    args = step_args(Batch(entries=((3, 1),), tokens=1, reqs=1, heads=4, kv_heads=2,
+                           head_dim=32, block=4), "cpu", torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU path"):
         kvpath.paged_attention(*args)
     with pytest.raises(RuntimeError, match="no CPU path"):
@@ -228,12 +227,11 @@ def test_newest_positions_assert() -> None:
     """kvpath.assert_newest_positions (the opt-in KVPATH_CHECK_POSITIONS check) accepts the
     sample plans and refuses a plan whose row sits at a wrong position, as kelpie's
     _assert_newest_positions does (on CPU tensors torch._assert_async raises at once)."""
-    from reference_sample import sample
-    from workloads import Batch
+    from workloads import Batch, step_args
 
     batch = Batch(entries=((16, 1), (63, 4), (5, 16)), tokens=24, reqs=4, heads=8, kv_heads=2,
                   head_dim=32, block=16)
-    args = sample(batch, "cpu", torch.float32, seed=3)
+    args = step_args(batch, "cpu", torch.float32, seed=3)
     rr, pos, qsl, lens = args[4], args[5], args[6], args[7]
     kvpath.assert_newest_positions(rr, pos, qsl, lens)
     bad = pos.clone()

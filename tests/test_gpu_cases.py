@@ -20,9 +20,8 @@ import torch
 import kvpath
 from helpers import within
 from oracle import attention as oracle
-from reference_sample import sample
 from test_gpu_path import BF16_ATOL, BF16_RTOL, say
-from workloads import Batch, reference_cases, synthetic
+from workloads import Batch, reference_cases, step_args, synthetic
 
 pytestmark = pytest.mark.gpu
 
@@ -32,10 +31,10 @@ CASES = reference_cases()
 @pytest.mark.parametrize("index", range(len(CASES)), ids=[label for label, _ in CASES])
 def test_reference_case(index) -> None:
     label, batch = CASES[index]
-    truth = oracle.paged_attention(*sample(batch, "cpu", torch.float64, seed=index))
-    ref = oracle.paged_attention(*sample(batch, "cpu", torch.bfloat16, seed=index))
+    truth = oracle.paged_attention(*step_args(batch, "cpu", torch.float64, seed=index))
+    ref = oracle.paged_attention(*step_args(batch, "cpu", torch.bfloat16, seed=index))
     budget = oracle.error_budget(truth, ref)
-    out = kvpath.paged_attention(*sample(batch, "cuda", torch.bfloat16, seed=index))
+    out = kvpath.paged_attention(*step_args(batch, "cuda", torch.bfloat16, seed=index))
     torch.cuda.synchronize()
     got = out.cpu()
     err = (got.double() - truth).abs().max().item()

@@ -17,9 +17,8 @@ import torch
 
 import kvpath
 from gpu_support import compact_cpu, dequantized
-from helpers import digest, golden_batch, within
-from reference_sample import sample
-from workloads import Batch, config_batch, copy_pairs, synthetic
+from helpers import digest, golden_args, golden_batch, within
+from workloads import Batch, config_batch, copy_pairs, step_args, synthetic
 from oracle import attention as oracle
 from oracle import kvbytes
 
@@ -129,7 +128,7 @@ def test_gather_bit_exact() -> None:
     say("gather")
     batch = Batch(entries=((100, 1), (37, 1), (5, 1)), tokens=4, reqs=4, heads=32, kv_heads=8,
                   head_dim=128, block=16, sinks=False)
-    args = sample(batch, "cuda", torch.bfloat16, seed=3)
+    args = step_args(batch, "cuda", torch.bfloat16, seed=3)
     kv_member, table = args[3], args[8]
     gk, gv = kvpath.kv_gather(kv_member, table)
     wk, wv = kvbytes.kv_gather(compact_member(kv_member), table.cpu(), table.shape[1])
@@ -352,7 +351,7 @@ def test_golden_cases_bf16(name, golden) -> None:
     meta, arrays = golden
     say("golden", name)
     batch = golden_batch(name, meta)
-    args = sample(batch, "cuda", torch.bfloat16, seed=meta[name]["seed"])
+    args = golden_args(name, golden, "cuda", torch.bfloat16)
     out = kvpath.paged_attention(*args)
     torch.cuda.synchronize()
     truth = torch.from_numpy(arrays[f"{name}/out_float64"]).double()
@@ -366,7 +365,7 @@ def test_golden_cases_bf16(name, golden) -> None:
     assert torch.equal(out[n:].cpu(), torch.zeros_like(out[n:].cpu()))
     # The pool after the append equals the oracle's (whose pool digest is the reference's, pinned
     # on the CPU), byte for byte, except the scratch row of page 0 that all pad rows race on.
-    cpu_args = sample(batch, "cpu", torch.bfloat16, seed=meta[name]["seed"])
+    cpu_args = golden_args(name, golden, "cpu", torch.bfloat16)
     oracle.write_kv(cpu_args[3], cpu_args[1], cpu_args[2], cpu_args[9])
     got, want = _arena_of(args[3]), _arena_of(cpu_args[3])
     assert torch.equal(got[1:], want[1:]), name
@@ -376,8 +375,8 @@ def test_golden_cases_bf16(name, golden) -> None:
 
 
 def _arena_of(member: torch.Tensor) -> torch.Tensor:
-    """The whole arena a sample() member views, on the CPU, as [pages, block, 2, 2, Hkv, D] raw
-    16-bit words (the layout sample() allocates)."""
+    """The whole arena a two-member step's member views, on the CPU, as [pages, block, 2, 2, Hkv,
+    D] raw 16-bit words."""
     pages, _, block, heads, dim = member.shape
     words = torch.empty(0, dtype=torch.int16, device=member.device).set_(member.untyped_storage())
     return words.cpu().reshape(pages, block, 2, 2, heads, dim)
@@ -388,8 +387,7 @@ def test_golden_cases_fp32(name, golden) -> None:
     """fp32 inputs (the generic VALU kernel): within the reference's fp32 budget of the truth."""
     meta, arrays = golden
     say("golden fp32", name)
-    batch = golden_batch(name, meta)
-    args = sample(batch, "cuda", torch.float32, seed=meta[name]["seed"])
+    args = golden_args(name, golden, "cuda", torch.float32)
     out = kvpath.paged_attention(*args)
     truth = torch.from_numpy(arrays[f"{name}/out_float64"]).double()
     ref = torch.from_numpy(arrays[f"{name}/out_float32"])
@@ -581,7 +579,7 @@ def test_prefill_shapes(dim, heads, entries, window, use_sinks, causal) -> None:
                   causal=causal)
     for part in (0, 1 << 16):
         say("prefill shape", dim, heads, entries, window, use_sinks, causal, "partition", part)
-        args = sample(batch, "cuda", torch.bfloat16, seed=dim + n_rows)
+        args = step_args(batch, "cuda", torch.bfloat16, seed=dim + n_rows)
         out = kvpath.paged_attention(*args, partition=part)
         torch.cuda.synchronize()
         assert torch.isfinite(out).all()
@@ -596,7 +594,7 @@ def test_verify_matches_decode_rows() -> None:
     ctx = 700
     verify = Batch(entries=((ctx, 16),), tokens=16, reqs=1, heads=32, kv_heads=8, head_dim=128,
                    block=16, sinks=False)
-    args = list(sample(verify, "cuda", torch.bfloat16, seed=12))
+    args = list(step_args(verify, "cuda", torch.bfloat16, seed=12))
     out_v = kvpath.paged_attention(*args)
     q, _, _, kv_member, rr, pos, qsl, lens, table, slots, window, sinks, causal = args
     # decode-shaped plan for the same entry's last position, pages already written
@@ -614,7 +612,7 @@ def test_window_sinks_causal_variants(window, use_sinks, causal) -> None:
     batch = Batch(entries=((300, 1), (129, 4), (5, 16), (1000, 2)), tokens=24, reqs=5,
                   heads=64, kv_heads=8, head_dim=64, block=16, window=window, sinks=use_sinks,
                   causal=causal)
-    args = sample(batch, "cuda", torch.bfloat16, seed=13)
+    args = step_args(batch, "cuda", torch.bfloat16, seed=13)
     out = kvpath.paged_attention(*args)
     _check_against_oracle(out, args, None, BF16_ATOL, BF16_RTOL, label=f"w{window}")
     assert torch.equal(out[batch.n_rows:].cpu(), torch.zeros_like(out[batch.n_rows:].cpu()))
@@ -631,7 +629,7 @@ def test_window_slid_out_pages_may_be_null(rows) -> None:
     batch = Batch(entries=tuple((n, rows) for n in ctx), tokens=len(ctx) * rows + 2,
                   reqs=len(ctx) + 1, heads=64, kv_heads=8, head_dim=64, block=16, window=window,
                   sinks=True)
-    args = list(sample(batch, "cuda", torch.bfloat16, seed=31))
+    args = list(step_args(batch, "cuda", torch.bfloat16, seed=31))
     q, k, v, kv_member, rr, pos, qsl, lens, table, slots, win, sinks, causal = args
     kvpath.write_kv(kv_member, k, v, slots)
     full = kvpath.attend(q, kv_member, rr, qsl, lens, table, win, sinks, causal)
@@ -662,7 +660,7 @@ def test_split_entry_points_match_attend(cfg) -> None:
     batch = Batch(entries=batch.entries[:4], tokens=sum(r for _, r in batch.entries[:4]) + 1,
                   reqs=5, heads=batch.heads, kv_heads=batch.kv_heads, head_dim=batch.head_dim,
                   block=batch.block, sinks=True)
-    q, k, v, kv_member, rr, pos, qsl, lens, table, slots, window, sinks, causal = sample(
+    q, k, v, kv_member, rr, pos, qsl, lens, table, slots, window, sinks, causal = step_args(
         batch, "cuda", torch.bfloat16, seed=40 + cfg)
     kvpath.write_kv(kv_member, k, v, slots)
     part = 0  # the library's split of each entry by its own length
@@ -704,9 +702,9 @@ def test_position_check_passes_valid_plans(monkeypatch) -> None:
     module = sys.modules["kvpath.paged_attention"]
     batch = Batch(entries=((300, 1), (129, 4), (5, 16), (1000, 2)), tokens=24, reqs=5,
                   heads=32, kv_heads=8, head_dim=128, block=16, sinks=False)
-    plain = kvpath.paged_attention(*sample(batch, "cuda", torch.bfloat16, seed=50))
+    plain = kvpath.paged_attention(*step_args(batch, "cuda", torch.bfloat16, seed=50))
     monkeypatch.setattr(module, "CHECK_POSITIONS", True)
-    checked = kvpath.paged_attention(*sample(batch, "cuda", torch.bfloat16, seed=50))
+    checked = kvpath.paged_attention(*step_args(batch, "cuda", torch.bfloat16, seed=50))
     torch.cuda.synchronize()
     assert torch.equal(plain.cpu(), checked.cpu())
 
@@ -826,10 +824,10 @@ def test_generic_kernel_partials(dtype, dim, part) -> None:
     say("generic partials", dtype, dim, part)
     batch = Batch(entries=((690, 1), (333, 4), (31, 1), (512, 3)), tokens=11, reqs=5, heads=8,
                   kv_heads=2, head_dim=dim, block=16, sinks=True)
-    args = sample(batch, "cuda", dtype, seed=dim + part)
+    args = step_args(batch, "cuda", dtype, seed=dim + part)
     out = kvpath.paged_attention(*args, partition=part)
     torch.cuda.synchronize()
-    truth = oracle.paged_attention(*sample(batch, "cpu", torch.float64, seed=dim + part))
+    truth = oracle.paged_attention(*step_args(batch, "cpu", torch.float64, seed=dim + part))
     got = out.double().cpu()
     assert torch.equal(out[batch.n_rows:].cpu(), torch.zeros_like(out[batch.n_rows:].cpu()))
     atol, rtol = {torch.float32: (2e-5, 1e-5), torch.float16: (1e-3, 1e-3),
@@ -928,8 +926,8 @@ def test_graph_capture_replays_a_new_plan() -> None:
                   block=16, sinks=False)
     second = Batch(entries=tuple(entries[::-1]), tokens=8, reqs=8, heads=32, kv_heads=8,
                    head_dim=128, block=16, sinks=False)
-    static = list(sample(first, "cuda", torch.bfloat16, seed=10))
-    fresh = sample(second, "cuda", torch.bfloat16, seed=11)
+    static = list(step_args(first, "cuda", torch.bfloat16, seed=10))
+    fresh = step_args(second, "cuda", torch.bfloat16, seed=11)
     kvpath.paged_attention(*static)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()

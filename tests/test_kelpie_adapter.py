@@ -84,10 +84,9 @@ def test_impl_refuses_cpu_like_the_op(fake_kelpie) -> None:
     import torch
 
     from kvpath import kelpie_adapter
-    from reference_sample import sample
-    from workloads import Batch
+    from workloads import Batch, step_args
 
-    args = sample(Batch(entries=((3, 1),), tokens=1, reqs=1, heads=4, kv_heads=2, head_dim=32,
-                        block=4), "cpu", torch.bfloat16)
+    args = step_args(Batch(entries=((3, 1),), tokens=1, reqs=1, heads=4, kv_heads=2,
+                           head_dim=32, block=4), "cpu", torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU path"):
         kelpie_adapter.mi355x_paged_attention(*args)

@@ -15,8 +15,7 @@ import torch
 from torch._subclasses.fake_tensor import FakeTensorMode
 
 import kvpath
-from reference_sample import SAMPLE_BATCH, sample
-from workloads import Batch, synthetic
+from workloads import SAMPLE_BATCH, Batch, step_args, synthetic
 
 DECODE = Batch(entries=((100, 1), (37, 1), (600, 1)), tokens=4, reqs=4, heads=32, kv_heads=8,
                head_dim=128, block=16, sinks=False)
@@ -33,7 +32,7 @@ def _fake_args(args: tuple, mode: FakeTensorMode) -> tuple:
 def test_fake_shape_rule(batch) -> None:
     """Under FakeTensorMode (no kernel runs) both ops give [T, H * D] in q's dtype on q's device
     (ops/paged_attention.py:248-267)."""
-    args = sample(batch, "cpu", torch.bfloat16)
+    args = step_args(batch, "cpu", torch.bfloat16)
     mode = FakeTensorMode()
     with mode:
         fake = _fake_args(args, mode)
@@ -55,7 +54,7 @@ def test_backward_refuses() -> None:
 def _samples(fp8: bool) -> list[tuple]:
     out = []
     if not fp8:  # the fp8 kernels need D of 64, 128 or 256; SAMPLE_BATCH has D 32
-        out.append((sample(SAMPLE_BATCH, "cuda", torch.bfloat16), None))
+        out.append((step_args(SAMPLE_BATCH, "cuda", torch.bfloat16), None))
     for i, batch in enumerate((DECODE, VERIFY)):
         step = synthetic(batch, "cuda", torch.bfloat16, seed=70 + i, pool_pages=128,
                          cache_dtype=torch.float8_e4m3fn if fp8 else None)
@@ -93,7 +92,7 @@ def test_opcheck(fp8) -> None:
 @pytest.mark.gpu
 def test_backward_through_the_op_raises() -> None:
     """q requiring grad: the forward runs, `.backward()` raises NotImplementedError."""
-    args = sample(DECODE, "cuda", torch.bfloat16)
+    args = step_args(DECODE, "cuda", torch.bfloat16)
     q = args[0].detach().requires_grad_(True)
     out = kvpath.paged_attention(q, *args[1:])
     assert out.requires_grad

@@ -1,8 +1,9 @@
 """The CPU attention oracle, pinned (oracle/attention.py).
 
-Against the reference's own golden vectors (tests/golden: its sample() and op body, fp64 / fp32 /
-bf16), against the mathematics (closed forms, an independent brute-force loop, invariance under a
-permutation of the pool's pages), and the plan contract (pad rows zero, the positions assert).
+Against the reference's own golden vectors (tests/golden: the inputs its seeded sample() drew and
+its op body's outputs on them, fp64 / fp32 / bf16), against the mathematics (closed forms, an
+independent brute-force loop, invariance under a permutation of the pool's pages), and the plan
+contract (pad rows zero, the positions assert).
 """
 
 from __future__ import annotations
@@ -13,15 +14,16 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import digest, golden_batch
-from reference_sample import sample
-from workloads import Batch
+from helpers import digest, golden_args
+from workloads import Batch, step_args
 from oracle import attention as oracle
+
+DTYPES = {"float64": torch.float64, "float32": torch.float32, "bfloat16": torch.bfloat16}
 
 
 def _outs(arrays: dict, name: str) -> dict[str, torch.Tensor]:
     out = {}
-    for tag in ("float64", "float32", "bfloat16"):
+    for tag in DTYPES:
         key = f"{name}/out_{tag}"
         if key in arrays:
             a = torch.from_numpy(arrays[key])
@@ -29,29 +31,27 @@ def _outs(arrays: dict, name: str) -> dict[str, torch.Tensor]:
     return out
 
 
-def test_sample_reproduces_reference_draws(golden) -> None:
-    """reference_sample.sample == the reference's sample() byte for byte, every case and dtype."""
+def test_golden_inputs_are_the_reference_draws(golden) -> None:
+    """The fixture's inputs, rebuilt at each dtype, are byte for byte the tensors the reference's
+    sample() returned at that dtype (sha256 of each, the member's whole arena included)."""
     meta, _ = golden
     for name, entry in meta.items():
-        batch = golden_batch(name, meta)
         for tag, want in entry["inputs"].items():
-            args = sample(batch, "cpu", getattr(torch, tag), seed=entry["seed"])
+            args = golden_args(name, golden, "cpu", DTYPES[tag])
             got = [digest(a) if isinstance(a, torch.Tensor) else a for a in args]
             assert got == want, (name, tag)
 
 
 def test_oracle_matches_reference_outputs(golden) -> None:
-    """The oracle on the same sample reproduces the reference's fp64 truth (to fp32 storage), its
-    fp32 output, its bf16 output within bf16 rounding, and its post-append pool bytes."""
+    """The oracle on the reference's inputs reproduces its fp64 truth, its fp32 output, its bf16
+    output within bf16 rounding, and its post-append pool bytes."""
     meta, arrays = golden
     for name, entry in meta.items():
-        batch = golden_batch(name, meta)
-        outs = _outs(arrays, name)
-        for tag, want in outs.items():
-            args = sample(batch, "cpu", getattr(torch, tag), seed=entry["seed"])
+        for tag, want in _outs(arrays, name).items():
+            args = golden_args(name, golden, "cpu", DTYPES[tag])
             got = oracle.paged_attention(*args)
             if tag == "float64":
-                torch.testing.assert_close(got.float(), want, rtol=1e-6, atol=1e-7)
+                torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-13)
             elif tag == "float32":
                 torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6)
             else:
@@ -62,10 +62,8 @@ def test_oracle_matches_reference_outputs(golden) -> None:
 
 def test_brute_force_agrees_with_oracle(golden) -> None:
     """An independent per-(row, head) Python loop gives the oracle's fp64 result."""
-    meta, _ = golden
     for name in ("sample_batch", "decode_window", "verify_ragged", "drafter", "prefill_mixed"):
-        batch = golden_batch(name, meta)
-        args = sample(batch, "cpu", torch.float64, seed=meta[name]["seed"])
+        args = golden_args(name, golden, "cpu", torch.float64)
         want = oracle.paged_attention(*args)
         q, _, _, kv_member, row_request, _, qsl, seq_lens, table, _, window, sinks, causal = args
         got = oracle.brute_force(q, kv_member, row_request, qsl, seq_lens, table, window, sinks,
@@ -74,9 +72,9 @@ def test_brute_force_agrees_with_oracle(golden) -> None:
 
 
 def _single_entry(ctx: int, rows: int, heads=4, kv_heads=2, dim=8, block=4, **kw) -> tuple:
-    return sample(Batch(entries=((ctx, rows),), tokens=rows, reqs=1, heads=heads,
-                        kv_heads=kv_heads, head_dim=dim, block=block, **kw), "cpu",
-                  torch.float64, seed=3)
+    return step_args(Batch(entries=((ctx, rows),), tokens=rows, reqs=1, heads=heads,
+                           kv_heads=kv_heads, head_dim=dim, block=block, **kw), "cpu",
+                     torch.float64, seed=3)
 
 
 def test_one_visible_key_returns_its_value() -> None:
@@ -122,7 +120,7 @@ def test_sink_with_one_key() -> None:
 def test_pad_rows_are_zero_and_masked_rows_zero() -> None:
     """Pad rows (row_request -1) are exactly 0, with and without sinks."""
     for sinks in (False, True):
-        args = sample(Batch(entries=((5, 2), (3, 1)), tokens=6, reqs=4, heads=4, kv_heads=2,
+        args = step_args(Batch(entries=((5, 2), (3, 1)), tokens=6, reqs=4, heads=4, kv_heads=2,
                             head_dim=8, block=4, sinks=sinks), "cpu", torch.float32, seed=1)
         out = oracle.paged_attention(*args)
         assert torch.equal(out[3:], torch.zeros_like(out[3:]))
@@ -133,10 +131,10 @@ def test_page_permutation_invariance() -> None:
     """Relabeling the pool's pages (table and pool permuted together) changes nothing."""
     batch = Batch(entries=((21, 3), (9, 1)), tokens=4, reqs=2, heads=4, kv_heads=2, head_dim=8,
                   block=4, window=0, sinks=True)
-    args = list(sample(batch, "cpu", torch.float64, seed=5))
+    args = list(step_args(batch, "cpu", torch.float64, seed=5))
     want = oracle.paged_attention(*[a.clone() if isinstance(a, torch.Tensor) and a.dim() != 5
                                     else a for a in args])
-    args = list(sample(batch, "cpu", torch.float64, seed=5))
+    args = list(step_args(batch, "cpu", torch.float64, seed=5))
     kv_member = args[3]
     pages = kv_member.shape[0]
     perm = torch.cat([torch.zeros(1, dtype=torch.long), torch.randperm(pages - 1) + 1])
@@ -157,7 +155,7 @@ def test_page_permutation_invariance() -> None:
 
 
 def test_positions_assert_refuses_a_bad_plan() -> None:
-    args = list(sample(Batch(entries=((5, 2),), tokens=2, reqs=1, heads=4, kv_heads=2,
+    args = list(step_args(Batch(entries=((5, 2),), tokens=2, reqs=1, heads=4, kv_heads=2,
                              head_dim=8, block=4), "cpu", torch.float32, seed=0))
     args[5] = args[5].clone()
     args[5][0] += 1
@@ -175,11 +173,11 @@ def test_error_budget_rule() -> None:
 
 def test_chunking_does_not_change_results() -> None:
     """The row-chunk bound is a memory bound only: one-row chunks give the same fp64 result."""
-    args = sample(Batch(entries=((30, 4), (12, 2)), tokens=8, reqs=3, heads=4, kv_heads=2,
+    args = step_args(Batch(entries=((30, 4), (12, 2)), tokens=8, reqs=3, heads=4, kv_heads=2,
                         head_dim=8, block=4, window=5), "cpu", torch.float64, seed=2)
     whole = oracle.paged_attention(*[a.clone() if isinstance(a, torch.Tensor) and a.dim() != 5
                                      else a for a in args])
-    args = sample(Batch(entries=((30, 4), (12, 2)), tokens=8, reqs=3, heads=4, kv_heads=2,
+    args = step_args(Batch(entries=((30, 4), (12, 2)), tokens=8, reqs=3, heads=4, kv_heads=2,
                         head_dim=8, block=4, window=5), "cpu", torch.float64, seed=2)
     tiny = oracle.paged_attention(*args, chunk_bytes=1)
     torch.testing.assert_close(tiny, whole, rtol=1e-13, atol=1e-15)

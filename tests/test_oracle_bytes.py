@@ -13,8 +13,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from reference_sample import sample
-from workloads import Batch
+from workloads import Batch, step_args
 from oracle import attention as oracle_attn
 from oracle import kvbytes
 
@@ -100,7 +99,7 @@ def test_token_valued_pool_reads_back_through_tables() -> None:
     its block table returns exactly the ids written (the check_core_loop.py:205-229 oracle)."""
     batch = Batch(entries=((13, 3), (0, 5), (30, 1)), tokens=10, reqs=4, heads=2, kv_heads=1,
                   head_dim=4, block=4)
-    args = sample(batch, "cpu", torch.float32, seed=7)
+    args = step_args(batch, "cpu", torch.float32, seed=7)
     kv_member, slots, table, qsl = args[3], args[9], args[8], args[6]
     seq_lens = args[7]
     # context rows get ids 1000*r + position, this step's rows the same rule
@@ -130,7 +129,7 @@ def test_gather_matches_index_select() -> None:
     """out[r, j] = K[table[r, j//block]*block + j%block] (ops:174-177 with index_select)."""
     batch = Batch(entries=((21, 2), (6, 1)), tokens=4, reqs=3, heads=4, kv_heads=2, head_dim=8,
                   block=4)
-    args = sample(batch, "cpu", torch.bfloat16, seed=2)
+    args = step_args(batch, "cpu", torch.bfloat16, seed=2)
     kv_member, table = args[3], args[8]
     width = table.shape[1]
     gk, gv = kvbytes.kv_gather(kv_member, table, width)

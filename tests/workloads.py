@@ -14,8 +14,10 @@ only: the library never imports this module.
 
 from __future__ import annotations
 
+import json
 import math
 from dataclasses import dataclass, field
+from pathlib import Path
 
 import torch
 
@@ -61,6 +63,7 @@ class Step:
     free_pages: torch.Tensor  # int32 page ids no entry uses (copy_blocks destinations)
     arena: torch.Tensor | None = None  # the whole arena the member views
     extra: dict = field(default_factory=dict)
+    member: int = 1  # which of the arena's layers args[3] views
 
     @property
     def kv_member(self) -> torch.Tensor:
@@ -176,7 +179,33 @@ def synthetic(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed
     args = (q, k, v, kv_member, row_request.to(device), positions.to(device),
             query_start_loc.to(device), seq_lens.to(device), table_dev, slot_mapping.to(device),
             b.window, sinks, b.causal)
-    return Step(args, kv_scale, b, pool, free_pages.to(device), arena)
+    return Step(args, kv_scale, b, pool, free_pages.to(device), arena, member=member)
+
+
+def moved(step: Step, device: str | torch.device) -> Step:
+    """`step` on `device`: the arena copied whole, the member re-viewed at the same strides."""
+    arena = step.arena.to(device)
+    kv_member = arena[:, :, step.member].permute(0, 2, 1, 3, 4)
+    args = tuple(kv_member if i == 3 else a.to(device) if isinstance(a, torch.Tensor) else a
+                 for i, a in enumerate(step.args))
+    scale = None if step.kv_scale is None else step.kv_scale.to(device)
+    return Step(args, scale, step.batch, step.pool_pages, step.free_pages.to(device), arena,
+                dict(step.extra), step.member)
+
+
+def step_args(batch: Batch, device: str | torch.device, dtype: torch.dtype, seed: int = 0,
+              **kw) -> tuple:
+    """The op's 13 arguments for a small `batch`, drawn on the CPU by `synthetic` and moved to
+    `device`: every device sees the same values, and since each value is drawn in fp32 and
+    rounded to bf16 before the cast to `dtype`, the float64 draw of a seed is the bf16 draw's
+    exact truth."""
+    return moved(synthetic(batch, "cpu", dtype, seed, **kw), device).args
+
+
+# A small odd case for the op's conventions (ops/paged_attention.py:370-373): GQA 2, one entry
+# with context + two rows, one decode row, a pad entry and a pad row, window 3, sinks.
+SAMPLE_BATCH = Batch(entries=((5, 2), (3, 1)), tokens=4, reqs=3, heads=4, kv_heads=2,
+                     head_dim=32, block=4, window=3)
 
 
 # ---- the BASELINE configurations -----------------------------------------------------------------
@@ -274,70 +303,38 @@ def copy_pairs(step: Step, n: int, seed: int = 0) -> tuple[torch.Tensor, torch.T
 
 # ---- the reference's per-op case list --------------------------------------------------------
 
-GPT_OSS_ATTN = dict(heads=64, kv_heads=8, head_dim=64, block=16)
+SHAPES = Path(__file__).resolve().parent / "golden" / "reference_shapes.json"
 
 
-def _reference_shapes(rng) -> list[tuple[str, dict]]:
-    """(label, Batch fields without window) over kelpie's build families (bench_attention.py:
-    62-84), contexts drawn from `rng` in the reference's draw order."""
-    max_seq, k_extra, decode = 512, 15, (1, 2, 4, 8)
-    shapes: list[tuple[str, dict]] = []
-    for r in decode:
-        shapes.append((f"decode R={r}", dict(entries=[(rng.randint(1, 700), 1) for _ in range(r)],
-                                             tokens=r, reqs=r)))
-    shapes.append(("decode R=8 (5 real)",
-                   dict(entries=[(rng.randint(1, 700), 1) for _ in range(5)], tokens=8, reqs=8)))
-    for t in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024):
-        n = -(-t // max_seq)
-        shapes.append((f"prefill T={t} fresh", dict(entries=[(0, t // n)] * n, tokens=t, reqs=n)))
-    shapes.append(("prefill T=512 chunk@300", dict(entries=[(300, 512)], tokens=512, reqs=1)))
-    shapes.append(("prefill T=128 mixed", dict(entries=[(0, 57), (400, 1), (33, 1), (129, 40),
-                                                        (5, 3)], tokens=128, reqs=8)))
-    shapes.append(("prefill T=1024 mixed", dict(entries=[(0, 300), (700, 1), (250, 511),
-                                                         (20, 100)], tokens=1024, reqs=8)))
-    for r in decode:
-        w = 1 + k_extra
-        full = [(rng.randint(1, 600), w) for _ in range(r)]
-        shapes.append((f"decode_extra R={r}", dict(entries=full, tokens=r * w, reqs=r)))
-        ragged = [(rng.randint(1, 600), 1 + rng.randint(0, k_extra)) for _ in range(r)]
-        shapes.append((f"decode_extra R={r} ragged", dict(entries=ragged, tokens=r * w, reqs=r)))
-    return [(label, {**kw, "entries": tuple(tuple(e) for e in kw["entries"])})
-            for label, kw in shapes]
+def _shape_table() -> dict:
+    """The reference per-op proof's shape tables, as its own functions returned them
+    (tests/golden/make_golden.py writes them from kelpie/scripts/bench_attention.py)."""
+    return json.loads(SHAPES.read_text())
+
+
+def _batch_of(kw: dict, **extra) -> Batch:
+    return Batch(**{**kw, "entries": tuple(tuple(e) for e in kw["entries"]), **extra})
 
 
 def reference_cases() -> list[tuple[str, Batch]]:
-    """The shapes kelpie's per-op proof grades `paged_attention` on (kelpie/scripts/
-    bench_attention.py:42-91): gpt-oss-20b attention (64 q / 8 kv heads, D 64, block 16, sinks)
-    at the build's step families for max_seq_len 512, 8 requests, 1024 batch tokens -- decode
-    R = 1..8 (and 5 real entries padded to 8), prefill T = 1..1024 (fresh prompts split over
-    512-row entries, a chunk after 300 cached keys, mixed prefill and decode), decode_extra R x 16
-    (DFlash's 1 + 15 rows; full and ragged) -- each with windows 0 and 128, and the drafter's
-    non-causal, sink-free call at the decode_extra shapes. Contexts come from random.Random(0) in
-    the reference's draw order, so the shapes are the reference's own; case i is drawn with
-    seed i, as the reference draws it."""
-    import random
-
-    cases = []
-    for label, kw in _reference_shapes(random.Random(0)):
-        for window in (0, 128):
-            cases.append((f"{label} w{window}", Batch(**kw, window=window, **GPT_OSS_ATTN)))
-        if label.startswith("decode_extra"):
-            cases.append((f"{label} drafter", Batch(**kw, sinks=False, causal=False,
-                                                    **GPT_OSS_ATTN)))
-    return cases
+    """The 62 shapes kelpie grades `paged_attention` on (kelpie/scripts/bench_attention.py:42-91):
+    gpt-oss-20b attention (64 q / 8 kv heads, D 64, block 16, sinks) at the build's step
+    families for max_seq_len 512, 8 requests, 1024 batch tokens -- decode R = 1..8 (and 5 real
+    entries padded to 8), prefill T = 1..1024 (fresh prompts split over 512-row entries, a chunk
+    after 300 cached keys, mixed prefill and decode), decode_extra R x 16 (DFlash's 1 + 15 rows;
+    full and ragged) -- each with windows 0 and 128, and the drafter's non-causal, sink-free call
+    at the decode_extra shapes. The contexts are the reference's own draws (random.Random(0))."""
+    return [(label, _batch_of(kw)) for label, kw in _shape_table()["cases"]]
 
 
 def reference_buckets() -> list[tuple[str, Batch, bool]]:
     """The reference's timing buckets (bench_attention.py:211-237): its shapes drawn from
     random.Random(1), without the chunked, mixed and 5-real cases, each at windows 0 and 128, as
     (label, batch, graphed): decode-shaped steps are timed as graph replays, prefill eagerly."""
-    import random
-
+    table = _shape_table()
     out = []
-    for label, kw in _reference_shapes(random.Random(1)):
-        if "chunk" in label or "mixed" in label or "(5 real)" in label:
-            continue
+    for label, kw in table["buckets"]:
         for window in (0, 128):
-            out.append((f"{label} w{window}", Batch(**kw, window=window, **GPT_OSS_ATTN),
+            out.append((f"{label} w{window}", _batch_of(kw, window=window, **table["attention"]),
                         not label.startswith("prefill")))
     return out
