@@ -239,7 +239,42 @@ def reference_buckets_line() -> dict:
             "heads, D 64, block 16, sinks; append + attention, one op call; us_per_layer_in_step: "
             f"one call per layer of a {CASE_LAYERS}-call graph)", "n_gpus": 1,
             "published": "kelpie/NOTES-attn.md:44-49 (A100/H100; context, not a target)",
-            "rows": rows}
+            "rows": rows, "memory": peak_memory_rows()}
+
+
+# The reference's memory shapes (bench_attention.py:244-245): its largest prefill, two ways.
+MEMORY_SHAPES = (("prefill T=1024 2x512", ((0, 512), (0, 512)), 1024, 2),
+                 ("prefill T=1024 1x1024", ((0, 1024),), 1024, 1))
+
+
+def peak_memory_rows() -> list[dict]:
+    """Peak device memory one eager op call allocates above its inputs, as the reference
+    measures it (bench_attention.py:241-261): torch's allocator peak after a reset, minus what
+    was allocated before the call. The op's output and its split-KV workspace are all it
+    allocates."""
+    import torch
+
+    import kvpath
+    from workloads import Batch, synthetic
+
+    rows = []
+    for label, entries, tokens, reqs in MEMORY_SHAPES:
+        batch = Batch(entries=entries, tokens=tokens, reqs=reqs, window=0, heads=64, kv_heads=8,
+                      head_dim=64, block=16)
+        args = synthetic(batch, "cuda", torch.bfloat16, seed=0).args
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        out = kvpath.paged_attention(*args)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - base
+        rows.append({"shape": label, "peak_bytes_above_inputs": int(peak),
+                     "peak_gib": round(peak / 2**30, 6), "output_bytes": out.numel() * 2})
+        log(f"memory {label}: {peak / 2**20:.2f} MiB above inputs (output "
+            f"{out.numel() * 2 / 2**20:.2f} MiB)")
+        del args, out
+        torch.cuda.empty_cache()
+    return rows
 
 
 def measured_traffic(kernel: str, workload: str) -> int | None:

@@ -59,13 +59,16 @@ def compact_cpu(args: tuple, entries: list[int] | None = None, kv_scale=None) ->
     return out, rows, scale_c
 
 
-def dequantized(member_fp8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
-    """An fp8 member (CPU) as f64 values e4m3 * scale[page, member, head], in an arena-layout
-    view (K/V interleaved per row) so the oracle's kv_views can flatten it."""
+def dequantized(member_fp8: torch.Tensor, scale: torch.Tensor,
+                dtype: torch.dtype = torch.float64) -> torch.Tensor:
+    """An fp8 member (CPU) as values e4m3 * scale[page, member, head] in `dtype`, in an
+    arena-layout view (K/V interleaved per row) so the oracle's kv_views can flatten it. The
+    product is formed in f64, where it is exact (4 + 24 significant bits), so an f32 result is
+    the f32 product rounded once, as an f32 dequantize computes it."""
     vals = member_fp8.to(torch.float32).to(torch.float64)
-    vals = vals * scale.to(torch.float64)[:, :, None, :, None]
+    vals = (vals * scale.to(torch.float64)[:, :, None, :, None]).to(dtype)
     pages, _, block, heads, dim = vals.shape
-    arena = torch.empty(pages, block, 1, KV_MEMBERS, heads, dim, dtype=torch.float64)
+    arena = torch.empty(pages, block, 1, KV_MEMBERS, heads, dim, dtype=dtype)
     member = arena[:, :, 0].permute(0, 2, 1, 3, 4)
     member.copy_(vals)
     return member

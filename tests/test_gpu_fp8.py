@@ -2,14 +2,17 @@
 attention over the same seeded K/V, kernels/ops/paged_attention.py:44-54, 160-240) -- the
 quantization error is inside what is graded.
 
-The gate is |out - truth| <= 5e-2 + 1e-2 |truth|. What an e4m3 cache can meet depends on the
-data, not only on the kernels: e4m3 keeps 3 mantissa bits, so a key element of magnitude x
-carries up to x/16 of rounding, and the score error it causes grows with |x|. On N(0,1) K/V
-(config 4's shape without its outliers) the scheme itself -- the C oracle's bytes dequantized and
-attended in fp64 -- stays within the gate, and so must the GPU. With config 4's 1% outliers x20
-the scheme's own error is many times the gate (keys near +-80 move their scores by ~0.4); no
-scale rule changes e4m3's relative precision, so there the GPU is graded on what it adds: its
-error against the truth may exceed the scheme's own by at most the gate, element by element.
+Config 4 as stated (1% outliers x20) is graded by the reference's own rule (kelpie bench/
+correctness.py:35-51): max|err| against the fp64 truth within max(2 x the error of the reference
+algorithm at the case's dtype, 5e-2 x max|truth|). At the case's dtype -- fp8 pages,
+dequantized, fp32 compute -- that is asserted. The same rule with the bf16 path's error in the
+budget, and the element-wise gate |out - truth| <= 5e-2 + 1e-2 |truth|, are reported: what an
+e4m3 cache can meet there depends on the data, not on the kernels. e4m3 keeps 3 mantissa bits,
+so a value rounds by up to 2^-4 of itself, more than the 5e-2 floor; an output dominated by one
+outlier of V carries that rounding whole, and a key outlier near +-60 moves its score by ~0.4.
+On N(0,1) K/V (config 4's shape without its outliers) the scheme itself -- the C oracle's bytes
+dequantized and attended in fp64 -- stays within the element-wise gate, and so must the GPU. In
+every case the GPU must be within the gate of the scheme's own exact result.
 
 A decode stream appends one row per step, so nearly every page's scale grows many times; scale
 growth is by powers of two (an exponent shift of the rows already in the page), so the stream's
@@ -73,12 +76,12 @@ def _fresh_scheme(cpu_args: tuple) -> torch.Tensor:
     return oracle.attend(q64, member64, rr, pos, qsl, lens, table, window, sinks.double(), causal)
 
 
-def _config4_pair(outliers: float):
+def _config4_pair(outliers: float, seed: int = 4):
     batch, extra = config_batch(4)
-    fp8 = synthetic(batch, "cuda", torch.bfloat16, seed=4, pool_pages=extra["pool_pages"],
+    fp8 = synthetic(batch, "cuda", torch.bfloat16, seed=seed, pool_pages=extra["pool_pages"],
                     outliers=outliers, cache_dtype=torch.float8_e4m3fn)
     out = kvpath.paged_attention_fp8(*fp8.args, fp8.kv_scale)
-    ref = synthetic(batch, "cuda", torch.bfloat16, seed=4, pool_pages=extra["pool_pages"],
+    ref = synthetic(batch, "cuda", torch.bfloat16, seed=seed, pool_pages=extra["pool_pages"],
                     outliers=outliers)
     kvpath.write_kv(ref.kv_member, ref.args[1], ref.args[2], ref.args[9])  # the step's rows
     torch.cuda.synchronize()
@@ -97,24 +100,63 @@ def test_config4_shape_meets_the_gate_against_unquantized_truth() -> None:
     assert ok, ratio
 
 
-def test_config4_outliers_add_nothing_beyond_the_scheme() -> None:
-    """Config 4 as stated (1% outliers x20): the GPU's error against the unquantized truth exceeds
-    the scheme's own error (the fp8 pages dequantized, attended in fp64) by at most the gate,
-    element by element; the strict ratio is reported."""
-    out, fp8, ref = _config4_pair(0.01)
-    rows, truth, scheme = _truth_and_scheme(ref.args, fp8.args, fp8.kv_scale, CONFIG4_SUBSET)
+def _reference_rule(out: torch.Tensor, ref_args: tuple, fp8_args: tuple, kv_scale: torch.Tensor,
+                    entries: list[int]) -> dict[str, float]:
+    """Config 4's output graded by the reference's rule (kelpie bench/correctness.py:35-51:
+    max|err| against the fp64 truth within max(2 x the error of the reference algorithm run at
+    the case's dtype, floor x max|truth|)), with BASELINE's fp8 floor 5e-2, two ways:
+    - `fp8`: the reference algorithm at the case's own dtype -- the fp8 pages dequantized to f32
+      (e4m3 x scale), fp32 compute, bf16 out, as oracle.attend computes any bf16 step;
+    - `bf16`: the reference algorithm at bf16 over the unquantized pool (the bf16 path's error).
+    Also the element-wise reading |err| <= 5e-2 + 1e-2 |truth|, and the GPU against the fp8
+    scheme evaluated exactly (fp64 over the dequantized pages)."""
+    cpu, rows, _ = compact_cpu(ref_args, entries)
+    (q, _, _, member, rr, pos, qsl, lens, table, _, window, sinks, causal) = cpu
+    q64, member64 = oracle.upcast((q, member))
+    truth = oracle.attend(q64, member64, rr, pos, qsl, lens, table, window, sinks.double(), causal)
+    ref_bf16 = oracle.attend(q, member, rr, pos, qsl, lens, table, window, sinks, causal)
+    cpu8, rows8, scale8 = compact_cpu(fp8_args, entries, kv_scale)
+    assert torch.equal(rows, rows8)
+    member8 = dequantized(cpu8[3], scale8)
+    scheme = oracle.attend(q64, member8, rr, pos, qsl, lens, table, window, sinks.double(), causal)
+    ref_fp8 = oracle.attend(q, dequantized(cpu8[3], scale8, torch.float32), rr, pos, qsl, lens,
+                            table, window, sinks, causal)
     got = out.cpu()[rows].double()
-    gate = FP8_ATOL + FP8_RTOL * truth.abs()
-    excess = ((got - truth).abs() - (scheme - truth).abs()) / gate
+    err = (got - truth).abs().max().item()
+    floor = FP8_ATOL * truth.abs().max().item()
+    budget_fp8 = max(2 * (ref_fp8.double() - truth).abs().max().item(), floor)
+    budget_bf16 = max(2 * (ref_bf16.double() - truth).abs().max().item(), floor)
     _, strict = within(got, truth, FP8_ATOL, FP8_RTOL)
-    _, scheme_ratio = within(scheme, truth, FP8_ATOL, FP8_RTOL)
-    _, kernel_ratio = within(got, scheme, FP8_ATOL, FP8_RTOL)
-    say("config 4 with outliers: strict err / tol", round(strict, 3), "scheme alone",
-        round(scheme_ratio, 3), "GPU vs scheme", round(kernel_ratio, 4), "worst excess / tol",
-        round(excess.max().item(), 4))
-    assert bool(torch.isfinite(got).all())
-    assert excess.max().item() <= 1.0
-    assert kernel_ratio <= 1.0
+    _, kernel = within(got, scheme, FP8_ATOL, FP8_RTOL)
+    return {"err": err, "max_truth": truth.abs().max().item(),
+            "ref_fp8_err": (ref_fp8.double() - truth).abs().max().item(),
+            "ref_bf16_err": (ref_bf16.double() - truth).abs().max().item(),
+            "vs_fp8_budget": err / budget_fp8, "vs_bf16_budget": err / budget_bf16,
+            "elementwise": strict, "vs_scheme": kernel}
+
+
+CONFIG4_GRADED = list(range(0, 128, 8))
+
+
+@pytest.mark.parametrize("seed", [4, 5, 6])
+def test_config4_graded_by_the_reference_rule(seed) -> None:
+    """Config 4 as stated (128 entries of 2-8k keys, 1% of K/V elements x20), a sixteen-entry
+    subset graded against the fp64 truth over the unquantized values. Asserted: the reference's
+    rule with the reference algorithm at the case's dtype (fp8 pages), and the GPU within the
+    gate of the fp8 scheme's own exact result. Reported: the rule with the bf16 path's error in
+    the budget, and the element-wise gate. Neither of those two can hold for every draw: e4m3
+    keeps 3 mantissa bits, so a value rounds by up to 2^-4 = 6.25% of itself, more than the 5e-2
+    floor, and an output dominated by one outlier value of V (|truth| up to ~60 here) inherits
+    that rounding whole."""
+    out, fp8, ref = _config4_pair(0.01, seed)
+    g = _reference_rule(out, ref.args, fp8.args, fp8.kv_scale, CONFIG4_GRADED)
+    say(f"config 4 seed {seed}: max err {g['err']:.4f} max|truth| {g['max_truth']:.2f} | "
+        f"err / budget(ref at fp8) {g['vs_fp8_budget']:.3f} | err / budget(bf16 path) "
+        f"{g['vs_bf16_budget']:.3f} | element-wise err / tol {g['elementwise']:.2f} | "
+        f"ref errors fp8 {g['ref_fp8_err']:.4f} bf16 {g['ref_bf16_err']:.4f} | GPU vs scheme "
+        f"{g['vs_scheme']:.4f}")
+    assert g["vs_fp8_budget"] <= 1.0, g
+    assert g["vs_scheme"] <= 1.0, g
 
 
 @pytest.mark.parametrize("dim,rows_last", [(128, 1), (128, 16), (64, 1), (256, 1)])
