@@ -22,6 +22,7 @@
  *                             compaction primitive this library adds, bit-exact page copies)
  *   kvpath_workspace_bytes    no counterpart (the reference allocates its scratch inside torch;
  *                             here the caller allocates it, so graph capture sees no allocation)
+ *   kvpath_workspace_bytes_max  the same, bounded over every step up to a bucket's size
  *   kvpath_split_plan         no counterpart in kelpie's op (it does not split a row's keys); the
  *                             per-sequence split follows kernels/vendored/cuda/vllm_attention/
  *                             triton_unified_attention.py:335-355
@@ -89,8 +90,17 @@ typedef struct kvpath_rows {
  *   seq_lens i32[R]     context length of each entry including this step's rows
  *   block_table i32[R, P]  page ids, row stride `table_stride` (elements); 0 = null page
  *   slot_mapping i32[T] flat slot page*block + offset for each row's K/V
- * A row's position is derived as seq_lens[r] - rows_r + i (its entry's newest positions), the
- * invariant kernels/ops/paged_attention.py:143-157 asserts; `positions` is not read.
+ *   positions i32[T]    each row's position (NULL: the plan is not checked)
+ * The kernels derive a row's position as seq_lens[r] - rows_r + i (its entry's newest
+ * positions).  With `positions` given, attention checks that invariant on every row, as
+ * kernels/ops/paged_attention.py:128, 143-157 asserts it on every call: a row that names an
+ * entry (row_request >= 0) must lie in that entry's rows, its entry's seq_len must fit the
+ * table row, positions[t] must be seq_lens[r] - rows_r + (t - qsl[r]), and when the attention
+ * launch appends the row itself (kvpath_paged_attention's fused append) and opts->check_slots
+ * is set, slot_mapping[t] must be that position's slot in the entry's table row.  A row that
+ * breaks the plan is written as NaN (every head) instead of its output, and bit 0 of
+ * *opts->plan_status is set; nothing traps.  The position check adds no dependent load to the
+ * output writers; the slot check adds one (a table read), so it is opt-in.
  */
 typedef struct kvpath_plan {
     const int32_t* row_request;
@@ -99,6 +109,7 @@ typedef struct kvpath_plan {
     const int32_t* block_table;
     const int32_t* slot_mapping;
     int64_t num_tokens, num_reqs, table_width, table_stride;
+    const int32_t* positions;
 } kvpath_plan;
 
 /* Attention options: `window` > 0 keeps keys (pos - window, pos] (0: no window; negative is
@@ -106,12 +117,16 @@ typedef struct kvpath_plan {
  * per-head sink logits (kernels/ops/paged_attention.py:215-240); `causal` = 0 lets every row
  * see its entry's whole context (the DFlash drafter). `partition_tokens` is a fixed split-KV
  * partition length for every entry, a multiple of 32; 0 lets the library split each entry by its
- * own length on the device (kvpath_split_plan). */
+ * own length on the device (kvpath_split_plan).  `plan_status` is NULL or a device int32 that
+ * the plan check ORs 1 into when a row breaks the plan (kvpath_plan; the caller clears it, and
+ * reads it whenever it syncs); `check_slots` != 0 adds the fused append's slot check to it. */
 typedef struct kvpath_attn_opts {
     int32_t window;
     const float* sinks;
     int32_t causal;
     int32_t partition_tokens;
+    int32_t* plan_status;
+    int32_t check_slots;
 } kvpath_attn_opts;
 
 /* Version of the ABI above (bumped on any change to a struct or signature). */
@@ -172,16 +187,31 @@ int32_t kvpath_split_plan(int64_t num_tokens, int64_t num_reqs, int64_t num_head
                           int32_t partition_tokens, kvpath_split* out);
 
 /*
- * Scratch bytes kvpath_attend / kvpath_paged_attention need for a step of this shape and
+ * Scratch bytes kvpath_attend / kvpath_paged_attention need for a step of exactly this shape and
  * partition_tokens (the split-KV partials: per row, q head and partition slot, D values and 2
- * floats; sized for f32 values, which a bf16 q halves in use).  -1 for a shape the library
- * refuses: a negative size, num_tokens / table_width / block_size of 2^31 or more (or a table
- * spanning 2^31 keys), more than 65535 entries, more than 2^16 heads or head dims, q heads not a
- * multiple of kv heads, a partition that is not a multiple of 32.
+ * floats; sized for f32 values, which a bf16 q halves in use).  The size is per exact shape: it
+ * does not grow monotonically with num_tokens or num_reqs (the split gives a step of more rows
+ * fewer partition slots per entry), so a workspace sized for one step may be too small for a
+ * smaller one; kvpath_workspace_bytes_max sizes one workspace for every step up to a bound.
+ * -1 for a shape the library refuses: a negative size, num_tokens / table_width / block_size of
+ * 2^31 or more (or a table spanning 2^31 keys), more than 65535 entries, more than 2^16 heads or
+ * head dims, q heads not a multiple of kv heads, a partition that is not a multiple of 32.
  */
 int64_t kvpath_workspace_bytes(int64_t num_tokens, int64_t num_reqs, int64_t num_heads,
                                int64_t kv_heads, int64_t head_dim, int64_t table_width,
                                int64_t block_size, int32_t partition_tokens);
+
+/*
+ * No counterpart in the reference (its scratch lives in torch's allocator).  Scratch bytes that
+ * serve every step of at most max_tokens rows and max_reqs entries with these heads, head dim,
+ * table width, block size and partition_tokens: the largest kvpath_workspace_bytes over those
+ * steps, so a caller that allocates once for its largest bucket covers its smaller buckets too.
+ * Non-decreasing in max_tokens and max_reqs.  Host arithmetic only (up to ~65 split choices per
+ * entry count), -1 for a shape kvpath_workspace_bytes refuses.
+ */
+int64_t kvpath_workspace_bytes_max(int64_t max_tokens, int64_t max_reqs, int64_t num_heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t table_width,
+                                   int64_t block_size, int32_t partition_tokens);
 
 /*
  * Attention only (replaces _attend and its mask/softmax, kernels/ops/paged_attention.py:

@@ -50,7 +50,7 @@ constexpr float kNegInf = -__builtin_huge_valf();
 // ---- the plan, per workgroup -------------------------------------------------------------------
 
 struct Entry {
-    int32_t q0, n_rows, seq_len, n_q;  // first row, rows, context length (clamped), q-rows
+    int32_t q0, n_rows, seq_len, n_q;  // first row, rows, context length, q-rows
     int32_t anchor, part;              // partition 0's first key, partition length (split_entry)
 };
 
@@ -66,9 +66,10 @@ __device__ __forceinline__ bool load_entry(const AttnArgs& a, int r, Entry& e) {
     e.q0 = q0;
     e.n_rows = q1 - q0;
     if (e.n_rows <= 0 || e.q0 < 0 || e.q0 + e.n_rows > a.T) return false;
-    const int64_t cap = a.table_width * a.c.block;
-    if (len > cap) len = cap;
-    if (len < e.n_rows) return false;  // not a plan: its rows must be its newest positions
+    // Not a plan: its rows must be its newest positions, and its keys must fit its table row
+    // (kelpie-core sizes tables for max_seq_len). Such an entry's rows are left to the dead-row
+    // writers (zeros, or NaN under the plan check).
+    if (len < e.n_rows || len > a.table_width * a.c.block) return false;
     e.seq_len = static_cast<int32_t>(len);
     e.n_q = e.n_rows * a.G;
     return true;
@@ -169,6 +170,37 @@ __device__ __forceinline__ bool row_live(const AttnArgs& a, int t, Entry& e) {
     const int r = a.row_request[t];
     return r >= 0 && r < a.R && load_entry(a, r, e) && t >= e.q0 && t < e.q0 + e.n_rows;
 }
+
+// The plan check, on every row an output writer writes when the plan carries `positions`: a row
+// that names an entry (row_request >= 0) must be one of that entry's rows (row_live: the entry
+// holds it, and its seq_len covers its rows and fits its table row), at its newest position
+// (positions[t] == seq_lens[r] - rows_r + (t - qsl[r]), the invariant kelpie's op asserts,
+// ops/paged_attention.py:143-157). With a.check_slots, a row this launch appends itself (k_new)
+// must also have slot_mapping[t] at that position's slot in the entry's table row (the slot the
+// kernels' reads of it assume; one more dependent load per row, so opt-in). `pos_t` is
+// positions[t], loaded by the caller beside its other per-row loads (plan_position); `live` and
+// `e` are row_live's result for t. A row that breaks the plan is written as NaN instead of its
+// attention output and sets bit 0 of *a.status (broken_plan).
+__device__ __forceinline__ int32_t plan_position(const AttnArgs& a, int t) {
+    return a.positions != nullptr ? a.positions[t] : 0;
+}
+
+__device__ __forceinline__ bool row_breaks_plan(const AttnArgs& a, int t, int32_t pos_t, bool live,
+                                                const Entry& e) {
+    if (a.positions == nullptr) return false;
+    if (!live) return a.row_request[t] >= 0;
+    const int pos = e.seq_len - e.n_rows + (t - e.q0);
+    if (pos_t != pos) return true;
+    if (!a.check_slots || a.k_new == nullptr) return false;
+    const int64_t page = a.table[static_cast<int64_t>(a.row_request[t]) * a.table_stride + pos / a.c.block];
+    return static_cast<int64_t>(a.slots[t]) != page * a.c.block + pos % a.c.block;
+}
+
+__device__ __forceinline__ void broken_plan(const AttnArgs& a) {
+    if (a.status != nullptr) __hip_atomic_fetch_or(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr uint32_t kNanBf16x2 = 0x7fc07fc0u;  // two quiet-NaN bf16 values
 
 __device__ __forceinline__ bool key_visible(const AttnArgs& a, const Entry& e, int qrow, int key) {
     const int pos = e.seq_len - e.n_rows + qrow / a.G;
@@ -499,7 +531,8 @@ __device__ __forceinline__ void wait_lds() {
 }
 
 // Direct output, grid slice z == R: every row that is not live gets exact zeros (what the reduce
-// writes for it). Threads test one row each; the workgroup then zeroes the dead rows it found
+// writes for it), or NaN when it names an entry it does not belong to under the plan check
+// (row_breaks_plan). Threads test one row each; the workgroup then writes the rows it found
 // together, 8 bytes (four bf16) per store. `list` holds NTH + 1 ints of LDS (NTH threads).
 template <int NTH>
 __device__ void zero_dead_rows(const AttnArgs& a, int* list) {
@@ -512,15 +545,21 @@ __device__ void zero_dead_rows(const AttnArgs& a, int* list) {
         __syncthreads();
         const int t = base + static_cast<int>(threadIdx.x);
         Entry e;
-        if (t < a.T && !row_live(a, t, e)) list[atomicAdd(&list[NTH], 1)] = t;
+        if (t < a.T && !row_live(a, t, e)) {
+            const bool broken = row_breaks_plan(a, t, 0, false, e);
+            if (broken) broken_plan(a);
+            list[atomicAdd(&list[NTH], 1)] = broken ? ~t : t;
+        }
         __syncthreads();
         const int n = list[NTH];
         for (int k = 0; k < n; ++k) {
-            const int64_t row = static_cast<int64_t>(list[k]) * a.out_srow;
+            const int tk = list[k];
+            const uint32_t fill = tk < 0 ? kNanBf16x2 : 0u;
+            const int64_t row = static_cast<int64_t>(tk < 0 ? ~tk : tk) * a.out_srow;
             for (int idx = static_cast<int>(threadIdx.x); idx < a.H * vecs; idx += NTH) {
                 const int hq = idx / vecs, v = idx - hq * vecs;
                 *reinterpret_cast<u32x2*>(out + row + static_cast<int64_t>(hq) * a.out_shead + 4 * v) =
-                    u32x2{0, 0};
+                    u32x2{fill, fill};
             }
         }
         __syncthreads();  // the list is rewritten next round
@@ -1172,7 +1211,10 @@ __device__ __forceinline__ void partition_body(const AttnArgs& a, char* lds) {
                 if constexpr (DIRECT) {
                     // One partition holds the row's keys: the reduce's arithmetic here, written
                     // only where the reduce would write it (row_request names this entry).
-                    if (a.row_request[t] != r) continue;
+                    // positions[t] is loaded beside row_request[t] (independent loads, one wait).
+                    const int32_t owner = a.row_request[t];
+                    const int32_t pos_t = plan_position(a, t);
+                    if (owner != r) continue;
                     float scale = 0.0f;  // no visible key: exact zeros
                     if (lsum > 0.0f) {
                         if (a.sinks != nullptr) {
@@ -1185,9 +1227,13 @@ __device__ __forceinline__ void partition_body(const AttnArgs& a, char* lds) {
                         }
                     }
                     o *= scale;
+                    u32x2 packed{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
+                    if (row_breaks_plan(a, t, pos_t, true, e)) {
+                        broken_plan(a);
+                        packed = u32x2{kNanBf16x2, kNanBf16x2};
+                    }
                     *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + static_cast<int64_t>(t) * a.out_srow +
-                                              static_cast<int64_t>(hq) * a.out_shead + d) =
-                        u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
+                                              static_cast<int64_t>(hq) * a.out_shead + d) = packed;
                     continue;
                 }
                 store_partial4(a, t, hq, p, d, o, lsum);
@@ -1344,14 +1390,17 @@ void attn_partition_verify(AttnArgs a) {
         const int full_lo = a.window > 0 ? pos_last - a.window + 1 : 0;
 
         u32x4 qb[TPW][KK];
-        // Direct output writes a row only where the reduce would (row_request names this entry).
+        // Direct output writes a row only where the reduce would (row_request names this entry);
+        // the row's position for the plan check is loaded here, so the load overlaps the blocks.
         bool own[TPW];
+        int32_t own_pos[TPW];
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
             const int qrow = tq0 + 16 * t + c;
             const bool ok = qrow < qr1;
             const int tok = e.q0 + (ok ? qrow / a.G : 0);
             own[t] = ok && (!a.direct || a.row_request[tok] == r);
+            own_pos[t] = a.direct ? plan_position(a, tok) : 0;
             const int hq = h * a.G + (ok ? qrow % a.G : 0);
             const char* qp = static_cast<const char*>(a.q) +
                              (static_cast<int64_t>(tok) * a.q_srow + static_cast<int64_t>(hq) * a.q_shead) * 2;
@@ -1645,11 +1694,13 @@ void attn_partition_verify(AttnArgs a) {
                 }
                 uint16_t* po = static_cast<uint16_t*>(a.out) + static_cast<int64_t>(tok) * a.out_srow +
                                static_cast<int64_t>(hq) * a.out_shead;
+                const bool broken = row_breaks_plan(a, tok, own_pos[t], true, e);
+                if (broken) broken_plan(a);
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     const f32x4 o = acc[t][nb] * scale;
                     *reinterpret_cast<u32x2*>(po + 16 * nb + 4 * g) =
-                        u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
+                        broken ? u32x2{kNanBf16x2, kNanBf16x2} : u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
                 }
                 continue;
             }
@@ -1801,8 +1852,10 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce(AttnArgs a) {
     const int n_pl = kReduceThreads / lanes_d;  // partition lanes
     const int pl = threadIdx.x / lanes_d, vi = threadIdx.x % lanes_d;
 
+    const int32_t pos_t = plan_position(a, t);
     Entry e;
     const bool live = row_live(a, t, e);
+    const bool broken = row_breaks_plan(a, t, pos_t, live, e);
     int p_lo = 0, p_hi = -1;
     if (live) {
         int lo, hi;
@@ -1916,6 +1969,10 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce(AttnArgs a) {
                 scale = 1.0f / l;
             }
         }
+        if (broken) {
+            scale = __builtin_nanf("");  // every product NaN, zeros included
+            if (vi == 0) broken_plan(a);
+        }
         for (int i = 0; i < vec; ++i)
             store_from_f32(a.out, out_base + v * vec + i, a.out_dt, o[i] * scale);
     }
@@ -1936,8 +1993,10 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce_few(AttnArgs a) {
     const int hq = blockIdx.y * heads_per_wg + static_cast<int>(threadIdx.x) / n_vec;
     const int v = static_cast<int>(threadIdx.x) % n_vec;
     if (hq >= a.H) return;
+    const int32_t pos_t = plan_position(a, t);
     Entry e;
     const bool live = row_live(a, t, e);
+    const bool broken = row_breaks_plan(a, t, pos_t, live, e);
     const int64_t out_base = static_cast<int64_t>(t) * a.out_srow + static_cast<int64_t>(hq) * a.out_shead + 4 * v;
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
     float scale = 0.0f;  // a dead row, or no visible key: exact zeros
@@ -2004,6 +2063,10 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce_few(AttnArgs a) {
             }
         }
     }
+    if (broken) {
+        scale = __builtin_nanf("");  // every product NaN, zeros included
+        if (threadIdx.x == 0) broken_plan(a);
+    }
     if (a.out_dt == DT_BF16) {
         u32x2 w;
         w[0] = static_cast<uint32_t>(f32_to_bf16(o[0] * scale)) | (static_cast<uint32_t>(f32_to_bf16(o[1] * scale)) << 16);
@@ -2025,8 +2088,10 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce_few_bf16x8(AttnArg
     const int hq = blockIdx.y * heads_per_wg + static_cast<int>(threadIdx.x) / n_vec;
     const int v = static_cast<int>(threadIdx.x) % n_vec;
     if (hq >= a.H) return;
+    const int32_t pos_t = plan_position(a, t);
     Entry e;
     const bool live = row_live(a, t, e);
+    const bool broken = row_breaks_plan(a, t, pos_t, live, e);
     const int64_t out_base = static_cast<int64_t>(t) * a.out_srow + static_cast<int64_t>(hq) * a.out_shead + 8 * v;
     f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = {0.0f, 0.0f, 0.0f, 0.0f};
     float scale = 0.0f;  // a dead row, or no visible key: exact zeros
@@ -2091,6 +2156,10 @@ __global__ __launch_bounds__(kReduceThreads) void attn_reduce_few_bf16x8(AttnArg
                 scale = 1.0f / l;
             }
         }
+    }
+    if (broken) {
+        scale = __builtin_nanf("");  // every product NaN, zeros included
+        if (threadIdx.x == 0) broken_plan(a);
     }
     const f32x4 a0 = o0 * scale, a1 = o1 * scale;
     *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + out_base) =
@@ -2210,6 +2279,30 @@ SplitChoice choose_split(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int6
     if (cap > 1 && cap % 2 == 0) cap += 1;
     const int64_t slots = std::min<int64_t>(cap, std::max<int64_t>(1, cdiv(keys, base)));
     return SplitChoice{static_cast<int32_t>(base), static_cast<int32_t>(slots), 0};
+}
+
+int64_t max_token_slots(int64_t max_tokens, int64_t max_reqs, int64_t q_heads, int64_t kv_heads,
+                        int64_t width, int64_t block, int32_t partition) {
+    if (max_tokens <= 0) return 0;
+    if (partition > 0 || max_reqs <= 0)  // the slots do not depend on the step's rows
+        return max_tokens * choose_split(max_tokens, std::max<int64_t>(1, max_reqs), q_heads, kv_heads,
+                                         width, block, partition).slots;
+    // choose_split reads a step's rows only through its row tiles per entry,
+    // ceil(T * G / (16 * R)): slots are constant while the tiles stay within one of the ranges
+    // {1}, [2, 4], [4g - 3, 4g] (g = 2..63) and [253, inf), so T * slots peaks at the largest T
+    // of each range, T <= 16 * t_hi * R / G, or at max_tokens.
+    const int64_t G = std::max<int64_t>(1, q_heads / std::max<int64_t>(1, kv_heads));
+    int64_t best = 0;
+    for (int64_t R = 1; R <= max_reqs; ++R) {
+        const auto at = [&](int64_t T) {
+            if (T >= 1 && T <= max_tokens)
+                best = std::max(best, T * choose_split(T, R, q_heads, kv_heads, width, block, 0).slots);
+        };
+        at(max_tokens);
+        at(16 * R / G);
+        for (int64_t g = 1; g < 64; ++g) at(64 * g * R / G);
+    }
+    return best;
 }
 
 int32_t grid_slots(int32_t window, int64_t n_tokens, int32_t part, int32_t slots) {

@@ -28,6 +28,11 @@ void* g_scratch_ptr[kMaxDevices] = {};
 
 // The current device's address of `scratch`, looked up once per device (with that device
 // current) and kept. Returns a HIP error when the device or the lookup fails.
+// The first call on a device may come while a stream is being captured (the entry point is for
+// code under hipGraph capture). The lookup is no stream operation, but it may load the code
+// object that holds `scratch`, which a capture in global or thread-local mode forbids; so this
+// thread's capture mode is relaxed for the lookup alone and restored after it, which leaves the
+// capture valid and records nothing into it.
 hipError_t scratch_ptr(void** out) {
     int dev = -1;
     hipError_t err = hipGetDevice(&dev);
@@ -35,8 +40,13 @@ hipError_t scratch_ptr(void** out) {
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (g_scratch_ptr[dev] == nullptr) {
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        err = hipThreadExchangeStreamCaptureMode(&mode);
+        if (err != hipSuccess) return err;
         void* p = nullptr;
-        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t lookup = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        err = hipThreadExchangeStreamCaptureMode(&mode);
+        if (lookup != hipSuccess) return lookup;
         if (err != hipSuccess) return err;
         g_scratch_ptr[dev] = p;
     }
@@ -287,6 +297,9 @@ int32_t attend_args(const kvpath_rows* q, const kvpath::CacheView& c, const kvpa
     a.window = opts ? opts->window : 0;
     a.causal = opts ? (opts->causal != 0) : 1;
     a.sinks = opts ? opts->sinks : nullptr;
+    a.positions = plan->positions;
+    a.status = opts ? opts->plan_status : nullptr;
+    a.check_slots = opts ? (opts->check_slots != 0) : 0;
     a.score_scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(c.d)));
     a.part = split.part;
     a.part_fixed = split.fixed;
@@ -345,7 +358,7 @@ int32_t paged_attention_impl(const kvpath_rows* q, const kvpath_rows* k, const k
 
 extern "C" {
 
-int32_t kvpath_abi_version(void) { return 3; }
+int32_t kvpath_abi_version(void) { return 4; }
 
 const char* kvpath_last_error(void) { return g_error.c_str(); }
 
@@ -425,6 +438,20 @@ int64_t kvpath_workspace_bytes(int64_t num_tokens, int64_t num_reqs, int64_t num
     const kvpath::SplitChoice sp = kvpath::choose_split(num_tokens, num_reqs, num_heads, kv_heads,
                                                         table_width, block_size, partition_tokens);
     return workspace_layout(num_tokens, num_heads, head_dim, sp.slots).total;
+}
+
+int64_t kvpath_workspace_bytes_max(int64_t max_tokens, int64_t max_reqs, int64_t num_heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t table_width,
+                                   int64_t block_size, int32_t partition_tokens) {
+    if (shape_problem(max_tokens, max_reqs, num_heads, kv_heads, head_dim, table_width, block_size,
+                      partition_tokens) != nullptr ||
+        kv_heads < 1 || num_heads % kv_heads != 0)
+        return -1;
+    const int64_t token_slots = kvpath::max_token_slots(max_tokens, max_reqs, num_heads, kv_heads,
+                                                        table_width, block_size, partition_tokens);
+    // T * H * slots partial rows at most: the layout of one row with that many slots bounds every
+    // step's (its sizes grow with T * slots alone).
+    return workspace_layout(1, num_heads, head_dim, token_slots).total;
 }
 
 int32_t kvpath_attend(const kvpath_rows* q, const kvpath_cache* cache, const kvpath_plan* plan,

@@ -85,6 +85,11 @@ struct AttnArgs {
     // normalizes and writes `out` itself, an extra grid slice (z == R) zeroes the rows no entry
     // owns, and no reduce runs.
     int32_t direct;
+    // The plan check (kvpath_plan::positions; nullptr: unchecked): the output writers write a row
+    // that breaks the plan as NaN and set bit 0 of *status (nullptr: no status word).
+    const int32_t* positions;
+    int32_t* status;
+    int32_t check_slots;     // also check a fused-append row's slot against its table slot
 };
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t s);
@@ -105,6 +110,10 @@ struct SplitChoice {
 // The split for a step of this shape; `partition` > 0 is a caller's fixed length.
 SplitChoice choose_split(int64_t n_tokens, int64_t n_reqs, int64_t q_heads, int64_t kv_heads,
                          int64_t width, int64_t block, int32_t partition);
+// The largest T * slots of any step with T <= max_tokens rows and R <= max_reqs entries of this
+// shape (a workspace for it serves every such step; T * slots alone is not monotone in T or R).
+int64_t max_token_slots(int64_t max_tokens, int64_t max_reqs, int64_t q_heads, int64_t kv_heads,
+                        int64_t width, int64_t block, int32_t partition);
 // Partition slots per entry the grid holds (AttnArgs::grid_parts): all `slots`, or with a window
 // only as many as an entry's window reaches. The partition and reduce kernels both derive each
 // entry's split from it, so it is set once with the rest of the arguments.

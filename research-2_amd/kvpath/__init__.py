@@ -15,6 +15,8 @@ from kvpath.paged_attention import (
     KV_MEMBERS,
     assert_newest_positions,
     attend,
+    check_plan_status,
+    clear_plan_status,
     copy_blocks,
     kv_gather,
     kv_views,
@@ -22,8 +24,11 @@ from kvpath.paged_attention import (
     no_sinks,
     paged_attention,
     paged_attention_fp8,
+    plan_status,
+    set_slot_check,
     split_plan,
     workspace_bytes,
+    workspace_bytes_max,
     write_kv,
 )
 
@@ -31,6 +36,8 @@ __all__ = [
     "KV_MEMBERS",
     "assert_newest_positions",
     "attend",
+    "check_plan_status",
+    "clear_plan_status",
     "copy_blocks",
     "kv_gather",
     "kv_views",
@@ -38,7 +45,10 @@ __all__ = [
     "no_sinks",
     "paged_attention",
     "paged_attention_fp8",
+    "plan_status",
+    "set_slot_check",
     "split_plan",
     "workspace_bytes",
+    "workspace_bytes_max",
     "write_kv",
 ]

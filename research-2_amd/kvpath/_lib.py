@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libkvpath.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, EINVAL, EUNSUPPORTED, ELAUNCH = 0, -1, -2, -3
 F32, F16, BF16, FP8_E4M3 = 0, 1, 2, 3
@@ -24,6 +24,7 @@ EXPORTS = (
     "kvpath_copy_blocks",
     "kvpath_split_plan",
     "kvpath_workspace_bytes",
+    "kvpath_workspace_bytes_max",
     "kvpath_attend",
     "kvpath_attend_partitions",
     "kvpath_attend_reduce",
@@ -71,6 +72,7 @@ class Plan(ctypes.Structure):
         ("num_reqs", ctypes.c_int64),
         ("table_width", ctypes.c_int64),
         ("table_stride", ctypes.c_int64),
+        ("positions", ctypes.c_void_p),
     ]
 
 
@@ -80,6 +82,8 @@ class AttnOpts(ctypes.Structure):
         ("sinks", ctypes.c_void_p),
         ("causal", ctypes.c_int32),
         ("partition_tokens", ctypes.c_int32),
+        ("plan_status", ctypes.c_void_p),
+        ("check_slots", ctypes.c_int32),
     ]
 
 
@@ -125,6 +129,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         "kvpath_copy_blocks": (i32, [p(Cache), vp, vp, i64, vp]),
         "kvpath_split_plan": (i32, [i64, i64, i64, i64, i64, i64, i32, p(Split)]),
         "kvpath_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64, i64, i32]),
+        "kvpath_workspace_bytes_max": (i64, [i64, i64, i64, i64, i64, i64, i64, i32]),
         "kvpath_attend": (i32, [p(Rows), p(Cache), p(Plan), p(AttnOpts), p(Rows), vp, i64, vp]),
         "kvpath_attend_partitions": (i32, [p(Rows), p(Cache), p(Plan), p(AttnOpts), vp, i64, vp]),
         "kvpath_attend_reduce": (i32, [p(Rows), p(Cache), p(Plan), p(AttnOpts), p(Rows), vp, i64,

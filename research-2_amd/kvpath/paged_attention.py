@@ -11,10 +11,13 @@ K = member[:, 0], V = member[:, 1]; any strides (the engine's arena views interl
 and span all layers per row, sdk/kv.py:163-224) as long as D is innermost. fp8 adds a scale
 tensor f32[pages, 2, Hkv] (`new_kv_scale`).
 
-PLAN (ops/paged_attention.py:10-13, 87-102): int32 `row_request[T]`, `query_start_loc[R+1]`,
-`seq_lens[R]`, `block_table[R, P]`, `slot_mapping[T]`. A row's position is derived on device as
-seq_lens[r] - rows_r + i; `positions` is accepted for signature parity and not read (as the
-vLLM adapter does, kernels/adapters/paged_attention_vllm.py:59-64).
+PLAN (ops/paged_attention.py:10-13, 87-102): int32 `row_request[T]`, `positions[T]`,
+`query_start_loc[R+1]`, `seq_lens[R]`, `block_table[R, P]`, `slot_mapping[T]`. The kernels derive
+a row's position as seq_lens[r] - rows_r + i (as the vLLM adapter does, kernels/adapters/
+paged_attention_vllm.py:59-64) and check `positions` against it on every call, as kelpie's op
+asserts it on every call (ops/paged_attention.py:128, 143-157): a row that breaks the plan is
+written as NaN and sets this device's plan-status word (`plan_status`, `check_plan_status`);
+nothing synchronizes and nothing traps, so the check sits in captured steps too.
 """
 
 from __future__ import annotations
@@ -27,10 +30,17 @@ import torch
 from kvpath import _lib
 
 KV_MEMBERS = 2
-# KVPATH_CHECK_POSITIONS=1: every op call also asserts on device that `positions` are the rows'
-# newest positions, as kelpie's op does (a device assert, no host sync, capture-safe). Off by
-# default: the kernels derive positions from seq_lens and never read `positions`.
-CHECK_POSITIONS = os.environ.get("KVPATH_CHECK_POSITIONS", "0") == "1"
+# KVPATH_CHECK_SLOTS=1 (or set_slot_check(True)): the kernels' plan check also compares each
+# fused-append row's slot_mapping with its position's slot in the block table, one more dependent
+# load per row in the output writers. Off by default; the position check always runs.
+_CHECK_SLOTS = os.environ.get("KVPATH_CHECK_SLOTS", "0") == "1"
+
+
+def set_slot_check(on: bool) -> bool:
+    """Turn the plan check's slot comparison on or off for later calls; returns the old setting."""
+    global _CHECK_SLOTS
+    old, _CHECK_SLOTS = _CHECK_SLOTS, bool(on)
+    return old
 
 _DTYPES = {
     torch.float32: _lib.F32,
@@ -119,8 +129,8 @@ def _rows(x: torch.Tensor, what: str) -> tuple[_lib.Rows, torch.Tensor]:
                      _dtype_code(x, what)), x
 
 
-def _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping, n_tokens: int
-          ) -> tuple[_lib.Plan, tuple[torch.Tensor, ...]]:
+def _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping, n_tokens: int,
+          positions=None) -> tuple[_lib.Plan, tuple[torch.Tensor, ...]]:
     keep = []
 
     def i32(t: torch.Tensor | None, what: str) -> torch.Tensor | None:
@@ -148,7 +158,8 @@ def _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping, n_t
     plan = _lib.Plan(
         ptr(i32(row_request, "row_request")), ptr(i32(query_start_loc, "query_start_loc")),
         ptr(i32(seq_lens, "seq_lens")), ptr(table), ptr(i32(slot_mapping, "slot_mapping")),
-        n_tokens, n_reqs, width, max(table.stride(0), width) if table is not None else width)
+        n_tokens, n_reqs, width, max(table.stride(0), width) if table is not None else width,
+        ptr(i32(positions, "positions")))
     return plan, tuple(keep)
 
 
@@ -163,23 +174,82 @@ def _workspace(device: torch.device, n_tokens: int, n_reqs: int, n_heads: int, k
     return ws[off: off + size] if size > 0 else ws[:1]
 
 
-def _opts(window: int, sinks: torch.Tensor, n_heads: int, causal: bool, partition: int
-          ) -> tuple[_lib.AttnOpts, torch.Tensor]:
+def _opts(window: int, sinks: torch.Tensor, n_heads: int, causal: bool, partition: int,
+          status: int | None = None) -> tuple[_lib.AttnOpts, torch.Tensor]:
     sink_ptr = None
     if sinks.numel() > 0:
         if sinks.shape != (n_heads,):
             raise ValueError(f"kvpath: sinks must be f32[{n_heads}], got {tuple(sinks.shape)}")
         sinks = sinks.to(torch.float32).contiguous()
         sink_ptr = sinks.data_ptr()
-    return _lib.AttnOpts(int(window), sink_ptr, int(bool(causal)), int(partition)), sinks
+    return _lib.AttnOpts(int(window), sink_ptr, int(bool(causal)), int(partition), status,
+                         int(_CHECK_SLOTS)), sinks
+
+
+# One plan-status word per device: an int32 the kernels' plan check ORs 1 into when a row breaks
+# the plan. Created (zeroed and synchronized) by the first op call on the device outside graph
+# capture; a call captured before it exists passes none (its bad rows are still written as NaN).
+_PLAN_STATUS: dict[int, torch.Tensor] = {}
+
+
+def _device_index(device: torch.device | int | None) -> int:
+    if isinstance(device, int):
+        return device
+    if device is None or device.index is None:
+        return torch.cuda.current_device()
+    return device.index
+
+
+def _plan_status_ptr(device: torch.device) -> int | None:
+    idx = _device_index(device)
+    word = _PLAN_STATUS.get(idx)
+    if word is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        word = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", idx))
+        torch.cuda.synchronize(idx)
+        _PLAN_STATUS[idx] = word
+    return word.data_ptr()
+
+
+def plan_status(device: torch.device | int | None = None) -> int:
+    """The bits the kernels' plan check has set on this device since the last clear (0: every
+    checked row was its entry's newest position at its table slot). Synchronizes the device."""
+    word = _PLAN_STATUS.get(_device_index(device))
+    if word is None:
+        return 0
+    torch.cuda.synchronize(word.device)
+    return int(word.item())
+
+
+def clear_plan_status(device: torch.device | int | None = None) -> None:
+    """Zero this device's plan-status word (synchronously)."""
+    word = _PLAN_STATUS.get(_device_index(device))
+    if word is not None:
+        torch.cuda.synchronize(word.device)
+        word.zero_()
+        torch.cuda.synchronize(word.device)
+
+
+def check_plan_status(device: torch.device | int | None = None) -> None:
+    """Raise if a call on this device broke the plan (kelpie's op fails its stream on the same
+    condition, ops/paged_attention.py:143-157; here the caller picks where it surfaces)."""
+    bits = plan_status(device)
+    if bits:
+        raise RuntimeError(f"kvpath: a paged_attention call broke the plan (status {bits:#x}): "
+                           f"some row is not its entry's newest position, or its slot_mapping "
+                           f"is not that position's table slot; its output rows are NaN")
 
 
 def assert_newest_positions(row_request: torch.Tensor, positions: torch.Tensor,
                             query_start_loc: torch.Tensor, seq_lens: torch.Tensor) -> None:
-    """kelpie's plan invariant (ops/paged_attention.py:143-157): every live row t of entry r
-    lies in [qsl[r], qsl[r+1]) and positions[t] == seq_lens[r] - rows_r + (t - qsl[r]). Checked
-    with torch._assert_async on the tensors' device: no host sync, so it can sit in a captured
-    step; a violation fails the stream (or raises at once on CPU tensors)."""
+    """kelpie's plan invariant as kelpie asserts it (ops/paged_attention.py:143-157): every live
+    row t of entry r lies in [qsl[r], qsl[r+1]) and positions[t] == seq_lens[r] - rows_r +
+    (t - qsl[r]). Checked with torch._assert_async on the tensors' device: no host sync, so it
+    can sit in a captured step; a violation fails the stream (or raises at once on CPU tensors).
+    The op itself does not call it: its kernels check the same invariant on every call and
+    answer a violation with NaN rows and the plan-status word (plan_status), which never traps;
+    this is for a caller that wants kelpie's failing stream instead."""
     live = row_request >= 0
     entry = row_request.clamp(min=0).long()
     t = torch.arange(row_request.shape[0], device=row_request.device)
@@ -209,6 +279,15 @@ def workspace_bytes(n_tokens: int, n_reqs: int, n_heads: int, kv_heads: int, hea
     at `partition` (0: the library's split)."""
     return _lib.load().kvpath_workspace_bytes(n_tokens, n_reqs, n_heads, kv_heads, head_dim, width,
                                               block, partition)
+
+
+def workspace_bytes_max(max_tokens: int, max_reqs: int, n_heads: int, kv_heads: int,
+                        head_dim: int, width: int, block: int, partition: int = 0) -> int:
+    """Bytes of split-KV scratch that serve every step of at most `max_tokens` rows and
+    `max_reqs` entries of this shape (kvpath_workspace_bytes_max): one allocation for a largest
+    bucket covers the smaller ones, which workspace_bytes of the largest shape alone does not."""
+    return _lib.load().kvpath_workspace_bytes_max(max_tokens, max_reqs, n_heads, kv_heads,
+                                                  head_dim, width, block, partition)
 
 
 # ---- entry points -------------------------------------------------------------------------------
@@ -261,10 +340,8 @@ def attend(q: torch.Tensor, kv_member: torch.Tensor, row_request: torch.Tensor,
 def _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens,
                           block_table, slot_mapping, window, sinks, causal=True, kv_scale=None,
                           partition=0) -> torch.Tensor:
-    dev = _on_device(q, k, v, kv_member, row_request, query_start_loc, seq_lens, block_table,
-                     slot_mapping)
-    if CHECK_POSITIONS:  # the kernels derive positions from query_start_loc and seq_lens
-        assert_newest_positions(row_request, positions, query_start_loc, seq_lens)
+    dev = _on_device(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens,
+                     block_table, slot_mapping)
     lib = _lib.load()
     n_tokens, n_heads, head_dim = q.shape
     cache = _cache(kv_member, kv_scale)
@@ -275,8 +352,9 @@ def _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_star
     outr = _lib.Rows(out.data_ptr(), n_tokens, n_heads, head_dim, out.stride(0), head_dim,
                      _dtype_code(out, "out"))
     plan, keep = _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping,
-                       n_tokens)
-    opts, sinks = _opts(window, sinks, n_heads, causal, max(0, int(partition)))
+                       n_tokens, positions)
+    opts, sinks = _opts(window, sinks, n_heads, causal, max(0, int(partition)),
+                        _plan_status_ptr(dev))
     ws = _workspace(dev, n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], head_dim,
                     block_table.shape[1], kv_member.shape[2], max(0, int(partition)))
     _lib.check("paged_attention", lib.kvpath_paged_attention(

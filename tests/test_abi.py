@@ -224,8 +224,8 @@ def test_python_layer_refuses_cpu_tensors() -> None:
 
 
 def test_newest_positions_assert() -> None:
-    """kvpath.assert_newest_positions (the opt-in KVPATH_CHECK_POSITIONS check) accepts the
-    sample plans and refuses a plan whose row sits at a wrong position, as kelpie's
+    """kvpath.assert_newest_positions (kelpie's own device assert, for callers that want it)
+    accepts the sample plans and refuses a plan whose row sits at a wrong position, as kelpie's
     _assert_newest_positions does (on CPU tensors torch._assert_async raises at once)."""
     from workloads import Batch, step_args
 
@@ -271,3 +271,45 @@ def test_split_choice_properties(lib) -> None:
             rows = T * H * slots
             want = (rows * dim * 4 + 255) // 256 * 256 + rows * 8
             assert lib.kvpath_workspace_bytes(T, R, H, hkv, dim, width, block, 0) == want, shape
+
+
+def test_workspace_bound_covers_every_smaller_step(lib) -> None:
+    """kvpath_workspace_bytes is per exact shape: at a 128k-key table (H 32 / Hkv 8 / D 128) a
+    five-entry decode step needs more than a six-, seven- or eight-entry one, because the split
+    gives more entries fewer slots each. kvpath_workspace_bytes_max(max_T, max_R, ...) is at
+    least kvpath_workspace_bytes of every step with T <= max_T rows and R <= max_R entries
+    (checked exhaustively on small bounds, by a seeded sample on large ones), and never shrinks
+    as either bound grows."""
+    exact = lib.kvpath_workspace_bytes
+    bound = lib.kvpath_workspace_bytes_max
+    shape = (32, 8, 128, 8192, 16, 0)  # H, Hkv, D, width (128k keys), block, partition
+    assert exact(5, 5, *shape) > exact(8, 8, *shape)  # the non-monotone case
+    assert bound(8, 8, *shape) >= max(exact(t, r, *shape) for t in range(1, 9) for r in range(1, 9))
+    for dims in ((32, 8, 128, 8192, 16, 0), (64, 8, 64, 64, 16, 0), (32, 8, 128, 300, 16, 0),
+                 (16, 1, 64, 2048, 32, 0), (32, 8, 128, 8192, 16, 512)):
+        for max_t, max_r in ((1, 1), (4, 4), (16, 8), (40, 3), (64, 64), (300, 16)):
+            b = bound(max_t, max_r, *dims)
+            worst = max(exact(t, r, *dims) for t in range(1, max_t + 1) for r in range(1, max_r + 1))
+            assert b >= worst, (dims, max_t, max_r, b, worst)
+            assert b == max(b, exact(max_t, max_r, *dims))
+    g = torch.Generator().manual_seed(9)
+    for _ in range(40):
+        max_t = int(torch.randint(1, 4096, (1,), generator=g))
+        max_r = int(torch.randint(1, 257, (1,), generator=g))
+        b = bound(max_t, max_r, *shape)
+        for _ in range(50):
+            t = int(torch.randint(1, max_t + 1, (1,), generator=g))
+            r = int(torch.randint(1, max_r + 1, (1,), generator=g))
+            assert exact(t, r, *shape) <= b, (t, r, max_t, max_r)
+    prev = 0
+    for max_t in range(1, 200):
+        b = bound(max_t, 64, *shape)
+        assert b >= prev, max_t
+        prev = b
+    prev = 0
+    for max_r in range(1, 200):
+        b = bound(256, max_r, *shape)
+        assert b >= prev, max_r
+        prev = b
+    assert bound(-1, 4, *shape) == -1 and bound(4, 4, 30, 8, 128, 64, 16, 0) == -1
+    assert kvpath.workspace_bytes_max(64, 64, 32, 8, 128, 8192, 16) == bound(64, 64, *shape)

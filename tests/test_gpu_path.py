@@ -692,21 +692,27 @@ def test_split_entry_points_match_attend(cfg) -> None:
         assert not torch.equal(got.cpu(), torch.zeros_like(got.cpu()))
 
 
-def test_position_check_passes_valid_plans(monkeypatch) -> None:
-    """With KVPATH_CHECK_POSITIONS on, the op asserts the plan's positions on device before its
-    kernels (kelpie's _assert_newest_positions); valid plans (decode, verify, pads) pass and the
-    output is unchanged. (A failing plan is tested on the CPU: on the GPU it would abort.)"""
-    import sys
-
-    say("position check")
-    module = sys.modules["kvpath.paged_attention"]
+def test_position_checks_pass_valid_plans() -> None:
+    """kelpie's own device assert (kvpath.assert_newest_positions, torch._assert_async) passes
+    the plan of a decode + verify + pad step on the GPU, and the op's output with the plan
+    check's opt-in slot comparison on equals its output without it, with the plan-status word
+    clear. (A failing plan is tested on the CPU for the assert, which on the GPU would abort the
+    stream, and in test_gpu_plan_check.py for the kernels' check.)"""
+    say("position checks")
     batch = Batch(entries=((300, 1), (129, 4), (5, 16), (1000, 2)), tokens=24, reqs=5,
                   heads=32, kv_heads=8, head_dim=128, block=16, sinks=False)
-    plain = kvpath.paged_attention(*step_args(batch, "cuda", torch.bfloat16, seed=50))
-    monkeypatch.setattr(module, "CHECK_POSITIONS", True)
-    checked = kvpath.paged_attention(*step_args(batch, "cuda", torch.bfloat16, seed=50))
+    args = step_args(batch, "cuda", torch.bfloat16, seed=50)
+    kvpath.assert_newest_positions(args[4], args[5], args[6], args[7])
+    kvpath.clear_plan_status()
+    plain = kvpath.paged_attention(*args)
+    old = kvpath.set_slot_check(True)
+    try:
+        checked = kvpath.paged_attention(*step_args(batch, "cuda", torch.bfloat16, seed=50))
+    finally:
+        kvpath.set_slot_check(old)
     torch.cuda.synchronize()
     assert torch.equal(plain.cpu(), checked.cpu())
+    assert kvpath.plan_status() == 0
 
 
 @pytest.mark.parametrize("window,ctx,cache", [

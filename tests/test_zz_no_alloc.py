@@ -21,8 +21,9 @@ from workloads import Batch, synthetic
 SCRATCH_BYTES = 64 << 20
 
 
-def _call(step, noalloc: bool) -> torch.Tensor:
-    """The op on step's pool through the C ABI, with or without a workspace."""
+def _call(step, noalloc: bool, sync: bool = True) -> torch.Tensor:
+    """The op on step's pool through the C ABI, with or without a workspace (and, with
+    sync=False, without synchronizing: a call that is being captured)."""
     lib = _lib.load()
     q, k, v, kv_member, rr, pos, qsl, lens, table, slots, window, sinks, causal = step.args
     cache = _cache(kv_member, step.kv_scale)
@@ -49,7 +50,8 @@ def _call(step, noalloc: bool) -> torch.Tensor:
             ctypes.byref(plan), ctypes.byref(opts), ctypes.byref(outr), ws.data_ptr(),
             ws.numel(), stream)
         _lib.check("paged_attention", st)
-    torch.cuda.synchronize()
+    if sync:
+        torch.cuda.synchronize()
     del qq, kk, vv, keep, sinks32
     return out
 
@@ -78,6 +80,54 @@ def test_noalloc_matches_the_workspace_entry_point() -> None:
         assert torch.equal(got.cpu().view(torch.int16), want.cpu().view(torch.int16))
         assert torch.equal(a.arena.cpu().view(torch.int16), b.arena.cpu().view(torch.int16))
         assert not bool(got[batch.n_rows:].ne(0).any())
+
+
+# Run in a fresh process, so that its first noalloc call on the device is the captured one.
+FIRST_CALL_CAPTURED = r"""
+import sys
+sys.path[:0] = [{root!r}, {root!r} + "/research-2_amd", {root!r} + "/tests"]
+import torch
+import test_zz_no_alloc as t
+from workloads import Batch
+batch = Batch(entries=((700, 1), (3000, 1), (40, 1), (1500, 1), (2047, 1)), tokens=6, reqs=6,
+              heads=32, kv_heads=8, head_dim=128, block=16, sinks=False)
+a, b = t._pair(batch, 93)
+arena0 = a.arena.clone()
+stream = torch.cuda.Stream()
+stream.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
+    out = t._call(a, noalloc=True, sync=False)
+torch.cuda.current_stream().wait_stream(stream)
+want = t._call(b, noalloc=False)
+for replay in range(3):
+    a.arena.copy_(arena0)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), want.cpu().view(torch.int16)), replay
+    assert torch.equal(a.arena.cpu().view(torch.int16), b.arena.cpu().view(torch.int16)), replay
+    eager = t._call(b, noalloc=True)  # eager work between the replays, through the same scratch
+    assert torch.equal(eager.cpu().view(torch.int16), want.cpu().view(torch.int16)), replay
+print("first call captured: ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_under_capture() -> None:
+    """In a fresh process, the first kvpath_paged_attention_noalloc call on the device is made
+    inside torch.cuda.graph capture (global mode), so the scratch's address is looked up under
+    capture: the capture stays valid, and each of three replays (eager calls in between) gives
+    the workspace entry point's output and pool, bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    proc = subprocess.run([sys.executable, "-c", FIRST_CALL_CAPTURED.format(root=root)],
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-4000:]
+    assert "first call captured: ok" in proc.stdout
 
 
 def test_noalloc_refuses_a_step_beyond_its_scratch() -> None:
