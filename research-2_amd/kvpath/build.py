@@ -1,5 +1,6 @@
 """Build recipe for libkvpath.so: every HIP source under csrc/ compiled for gfx950 and linked
-in-tree next to this file (kvpath/libkvpath.so), where `kvpath._lib` loads it.
+in-tree next to this file (kvpath/libkvpath.so), where `kvpath._lib` loads it; then
+libkvpath_torch.so, the torch.ops.kvpath registrations over its C ABI (csrc/kvpath_torch.cpp).
 
     python -m kvpath.build          # from research-2_amd/, or via __graft_entry__.build()
 
@@ -24,6 +25,8 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE.parent / "csrc"
 BUILD_DIR = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libkvpath.so"
+TORCH_OPS = PACKAGE / "libkvpath_torch.so"
+TORCH_OPS_SOURCE = CSRC / "kvpath_torch.cpp"
 ARCH = "gfx950"
 
 # Every device compile: packed-fp32 instructions off (hipcc alone may emit them; the host pass
@@ -88,6 +91,33 @@ def refuse_hazards(assembly: dict[str, str]) -> None:
                              "not linking libkvpath.so:\n" + "\n".join(lines))
 
 
+def build_torch_ops(verbose: bool = False) -> Path:
+    """libkvpath_torch.so: the torch.ops.kvpath registrations (csrc/kvpath_torch.cpp), host C++
+    against this interpreter's torch headers and libraries, linked to libkvpath.so beside it (its
+    rpath is its own directory, so the loader reuses the libkvpath.so ctypes loads)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    includes = cpp_extension.include_paths()
+    if "/opt/rocm/include" not in includes:
+        includes.append("/opt/rocm/include")
+    libdir = cpp_extension.library_paths()[0]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = TORCH_OPS.with_suffix(".so.tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", "-Wall", "-Wno-unused-function",
+           *[f"-I{d}" for d in includes], str(TORCH_OPS_SOURCE), "-o", str(tmp),
+           f"-L{PACKAGE}", "-l:libkvpath.so", f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch_cpu",
+           "-ltorch", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build of {TORCH_OPS.name} failed:\n{proc.stderr[-6000:]}")
+    os.replace(tmp, TORCH_OPS)
+    if verbose:
+        print(f"built {TORCH_OPS}", flush=True)
+    return TORCH_OPS
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every csrc/*.hip, scan its assembly, and link libkvpath.so. Always recompiles (it
     is the build check)."""
@@ -113,6 +143,7 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY} from {len(srcs)} sources", flush=True)
+    build_torch_ops(verbose)
     return LIBRARY
 
 

@@ -18,29 +18,50 @@ paged_attention_vllm.py:59-64) and check `positions` against it on every call, a
 asserts it on every call (ops/paged_attention.py:128, 143-157): a row that breaks the plan is
 written as NaN and sets this device's plan-status word (`plan_status`, `check_plan_status`);
 nothing synchronizes and nothing traps, so the check sits in captured steps too.
+
+The two ops, torch.ops.kvpath.paged_attention and paged_attention_fp8, are registered in C++
+(csrc/kvpath_torch.cpp, built into libkvpath_torch.so beside libkvpath.so): the dispatcher calls
+the C ABI with no Python frame between the caller and the launch. Their fake (meta) rules are
+registered here. The other entry points (write_kv, attend, kv_gather, copy_blocks) bind the C
+ABI through ctypes (_lib).
 """
 
 from __future__ import annotations
 
 import ctypes
 import os
+from pathlib import Path
 
 import torch
 
 from kvpath import _lib
 
 KV_MEMBERS = 2
-# KVPATH_CHECK_SLOTS=1 (or set_slot_check(True)): the kernels' plan check also compares each
-# fused-append row's slot_mapping with its position's slot in the block table, one more dependent
-# load per row in the output writers. Off by default; the position check always runs.
-_CHECK_SLOTS = os.environ.get("KVPATH_CHECK_SLOTS", "0") == "1"
+TORCH_OPS = Path(__file__).resolve().parent / "libkvpath_torch.so"
+
+
+def _load_ops() -> None:
+    """Register torch.ops.kvpath (libkvpath_torch.so, linked to libkvpath.so); raises, naming the
+    build command, when either library is missing."""
+    _lib.load()
+    if not TORCH_OPS.exists():
+        raise RuntimeError(f"{TORCH_OPS.name} not found at {TORCH_OPS}: build it first "
+                           f"(python -c 'import __graft_entry__ as g; g.build()' at the repo root)")
+    torch.ops.load_library(str(TORCH_OPS))
+
+
+_load_ops()
 
 
 def set_slot_check(on: bool) -> bool:
-    """Turn the plan check's slot comparison on or off for later calls; returns the old setting."""
-    global _CHECK_SLOTS
-    old, _CHECK_SLOTS = _CHECK_SLOTS, bool(on)
-    return old
+    """Turn the plan check's slot comparison on or off for later op calls (every thread);
+    returns the old setting. It compares each fused-append row's slot_mapping with its position's
+    slot in the block table, one more dependent load per row in the output writers, so it is off
+    unless KVPATH_CHECK_SLOTS=1 or this turns it on; the position check always runs."""
+    return bool(torch.ops.kvpath.set_check_slots(bool(on)))
+
+
+set_slot_check(os.environ.get("KVPATH_CHECK_SLOTS", "0") == "1")
 
 _DTYPES = {
     torch.float32: _lib.F32,
@@ -182,14 +203,7 @@ def _opts(window: int, sinks: torch.Tensor, n_heads: int, causal: bool, partitio
             raise ValueError(f"kvpath: sinks must be f32[{n_heads}], got {tuple(sinks.shape)}")
         sinks = sinks.to(torch.float32).contiguous()
         sink_ptr = sinks.data_ptr()
-    return _lib.AttnOpts(int(window), sink_ptr, int(bool(causal)), int(partition), status,
-                         int(_CHECK_SLOTS)), sinks
-
-
-# One plan-status word per device: an int32 the kernels' plan check ORs 1 into when a row breaks
-# the plan. Created (zeroed and synchronized) by the first op call on the device outside graph
-# capture; a call captured before it exists passes none (its bad rows are still written as NaN).
-_PLAN_STATUS: dict[int, torch.Tensor] = {}
+    return _lib.AttnOpts(int(window), sink_ptr, int(bool(causal)), int(partition), status), sinks
 
 
 def _device_index(device: torch.device | int | None) -> int:
@@ -200,35 +214,26 @@ def _device_index(device: torch.device | int | None) -> int:
     return device.index
 
 
-def _plan_status_ptr(device: torch.device) -> int | None:
-    idx = _device_index(device)
-    word = _PLAN_STATUS.get(idx)
-    if word is None:
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        word = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", idx))
-        torch.cuda.synchronize(idx)
-        _PLAN_STATUS[idx] = word
-    return word.data_ptr()
+def _status_word(device: torch.device | int | None) -> torch.Tensor:
+    """This device's plan-status word: an int32 the kernels' plan check ORs 1 into, created
+    (zeroed) by the op's first call on the device outside graph capture, or here."""
+    return torch.ops.kvpath.plan_status_word(_device_index(device))
 
 
 def plan_status(device: torch.device | int | None = None) -> int:
     """The bits the kernels' plan check has set on this device since the last clear (0: every
     checked row was its entry's newest position at its table slot). Synchronizes the device."""
-    word = _PLAN_STATUS.get(_device_index(device))
-    if word is None:
-        return 0
+    word = _status_word(device)
     torch.cuda.synchronize(word.device)
     return int(word.item())
 
 
 def clear_plan_status(device: torch.device | int | None = None) -> None:
     """Zero this device's plan-status word (synchronously)."""
-    word = _PLAN_STATUS.get(_device_index(device))
-    if word is not None:
-        torch.cuda.synchronize(word.device)
-        word.zero_()
-        torch.cuda.synchronize(word.device)
+    word = _status_word(device)
+    torch.cuda.synchronize(word.device)
+    word.zero_()
+    torch.cuda.synchronize(word.device)
 
 
 def check_plan_status(device: torch.device | int | None = None) -> None:
@@ -337,63 +342,20 @@ def attend(q: torch.Tensor, kv_member: torch.Tensor, row_request: torch.Tensor,
     return out
 
 
-def _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens,
-                          block_table, slot_mapping, window, sinks, causal=True, kv_scale=None,
-                          partition=0) -> torch.Tensor:
-    dev = _on_device(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens,
-                     block_table, slot_mapping)
-    lib = _lib.load()
-    n_tokens, n_heads, head_dim = q.shape
-    cache = _cache(kv_member, kv_scale)
-    qr, qq = _rows(q, "q")
-    kr, kk = _rows(k, "k")
-    vr, vv = _rows(v, "v")
-    out = torch.empty(n_tokens, n_heads * head_dim, dtype=q.dtype, device=dev)
-    outr = _lib.Rows(out.data_ptr(), n_tokens, n_heads, head_dim, out.stride(0), head_dim,
-                     _dtype_code(out, "out"))
-    plan, keep = _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping,
-                       n_tokens, positions)
-    opts, sinks = _opts(window, sinks, n_heads, causal, max(0, int(partition)),
-                        _plan_status_ptr(dev))
-    ws = _workspace(dev, n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], head_dim,
-                    block_table.shape[1], kv_member.shape[2], max(0, int(partition)))
-    _lib.check("paged_attention", lib.kvpath_paged_attention(
-        ctypes.byref(qr), ctypes.byref(kr), ctypes.byref(vr), ctypes.byref(cache),
-        ctypes.byref(plan), ctypes.byref(opts), ctypes.byref(outr), ws.data_ptr(), ws.numel(),
-        _stream(dev)))
-    del qq, kk, vv, keep
-    return out
+# kelpie::paged_attention's contract (ops/paged_attention.py:67-109) on HIP, registered in C++:
+# append k/v at slot_mapping into `kv_member` (in place), then paged causal GQA attention ->
+# [T, H * D] in q.dtype, pad rows exactly zero. Same 13 arguments, same order and meaning; the
+# optional trailing `partition` (split-KV partition length in keys, 0 = the library's split of
+# each entry by its own length) is this build's tuning knob and changes no result beyond fp32
+# rounding. paged_attention_fp8 takes the 13 arguments plus an fp8 member's scales
+# f32[pages, 2, Hkv] (`new_kv_scale`): k/v are quantized on append, dequantized in-kernel.
+# Backward raises NotImplementedError: the op is inference-only, as kelpie's is
+# (ops/paged_attention.py:380-385).
+paged_attention = torch.ops.kvpath.paged_attention
+paged_attention_fp8 = torch.ops.kvpath.paged_attention_fp8
 
 
-@torch.library.custom_op("kvpath::paged_attention", mutates_args=("kv_member",))
-def paged_attention(  # noqa: PLR0913
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    kv_member: torch.Tensor,
-    row_request: torch.Tensor,
-    positions: torch.Tensor,
-    query_start_loc: torch.Tensor,
-    seq_lens: torch.Tensor,
-    block_table: torch.Tensor,
-    slot_mapping: torch.Tensor,
-    window: int,
-    sinks: torch.Tensor,
-    causal: bool = True,
-    partition: int = 0,
-) -> torch.Tensor:
-    """kelpie::paged_attention's contract (ops/paged_attention.py:67-109) on HIP: append k/v at
-    slot_mapping into `kv_member` (in place), then paged causal GQA attention -> [T, H * D] in
-    q.dtype, pad rows exactly zero. Same 13 arguments, same order and meaning; the optional
-    trailing `partition` (split-KV partition length in keys, 0 = the library's choice) is this
-    build's tuning knob (a fixed split-KV partition length in keys; 0 = the library's split of
-    each entry by its own length) and changes no result beyond fp32 rounding."""
-    return _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_start_loc,
-                                 seq_lens, block_table, slot_mapping, window, sinks, causal, None,
-                                 partition)
-
-
-@paged_attention.register_fake
+@torch.library.register_fake("kvpath::paged_attention")
 def _fake(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens, block_table,
           slot_mapping, window, sinks, causal=True, partition=0):
     """The shape rule (ops/paged_attention.py:248-267): [T, H * D] in q's dtype."""
@@ -402,58 +364,12 @@ def _fake(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens,
     return torch.empty(q.shape[0], q.shape[1] * q.shape[2], dtype=q.dtype, device=q.device)
 
 
-@torch.library.custom_op("kvpath::paged_attention_fp8", mutates_args=("kv_member", "kv_scale"))
-def paged_attention_fp8(  # noqa: PLR0913
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    kv_member: torch.Tensor,
-    row_request: torch.Tensor,
-    positions: torch.Tensor,
-    query_start_loc: torch.Tensor,
-    seq_lens: torch.Tensor,
-    block_table: torch.Tensor,
-    slot_mapping: torch.Tensor,
-    window: int,
-    sinks: torch.Tensor,
-    causal: bool,
-    kv_scale: torch.Tensor,
-    partition: int = 0,
-) -> torch.Tensor:
-    """The op over an fp8 (float8_e4m3fn) member: the 13 arguments above plus its scales
-    f32[pages, 2, Hkv] (`new_kv_scale`). k/v are quantized on append, dequantized in-kernel."""
-    return _paged_attention_impl(q, k, v, kv_member, row_request, positions, query_start_loc,
-                                 seq_lens, block_table, slot_mapping, window, sinks, causal,
-                                 kv_scale, partition)
-
-
-@paged_attention_fp8.register_fake
+@torch.library.register_fake("kvpath::paged_attention_fp8")
 def _fake_fp8(q, k, v, kv_member, row_request, positions, query_start_loc, seq_lens, block_table,
               slot_mapping, window, sinks, causal, kv_scale, partition=0):
     del k, v, kv_member, row_request, positions, query_start_loc, seq_lens, block_table
     del slot_mapping, window, sinks, causal, kv_scale, partition
     return torch.empty(q.shape[0], q.shape[1] * q.shape[2], dtype=q.dtype, device=q.device)
-
-
-def _backward(ctx, *grads):
-    """The op is inference-only, as kelpie's is (ops/paged_attention.py:380-385): a backward
-    raises, naming that, instead of failing as a missing autograd formula."""
-    del ctx, grads
-    raise NotImplementedError("kvpath::paged_attention has no backward: the paged-KV path is "
-                              "inference-only (kelpie defers training to its train-step branch)")
-
-
-def _setup_context(ctx, inputs, output) -> None:
-    del ctx, inputs, output
-
-
-# torch.library refuses register_autograd on an op that mutates an argument (kv_member), the same
-# wall kelpie's op registry meets and answers by keeping the raising backward on its own op
-# object (kernels/op.py:101-113). Here the backward is given to the op's generated autograd
-# function directly: it only ever raises, so no gradient semantics of the mutation are implied.
-for _op in (paged_attention, paged_attention_fp8):
-    _op._backward_fn = _backward
-    _op._setup_context_fn = _setup_context
 
 
 def kv_gather(kv_member: torch.Tensor, block_table: torch.Tensor, width: int | None = None

@@ -44,11 +44,25 @@ def test_fake_shape_rule(batch) -> None:
         assert o.dtype == torch.bfloat16 and o.device.type == "cuda"
 
 
-def test_backward_refuses() -> None:
-    """Both ops carry a backward, and it raises NotImplementedError naming the op."""
-    for op in (kvpath.paged_attention, kvpath.paged_attention_fp8):
-        with pytest.raises(NotImplementedError, match="no backward"):
-            op._backward_fn(None, torch.zeros(1))
+def test_ops_are_registered_for_every_key_they_need() -> None:
+    """Both ops (registered in C++, libkvpath_torch.so) have a ROCm kernel, a CPU kernel that
+    refuses, an Autograd kernel (whose backward raises, exercised on the GPU below) and a fake;
+    the schema is kelpie's 13 arguments with kv_member (and kv_scale) the only ones written."""
+    from torch._library.simple_registry import singleton
+
+    for name in ("kvpath::paged_attention", "kvpath::paged_attention_fp8"):
+        for key in ("CUDA", "CPU", "Autograd"):
+            assert torch._C._dispatch_has_kernel_for_dispatch_key(name, key), (name, key)
+        assert singleton.find(name).fake_impl.kernel is not None, name
+    schema = torch.ops.kvpath.paged_attention.default._schema
+    assert [a.name for a in schema.arguments] == [
+        "q", "k", "v", "kv_member", "row_request", "positions", "query_start_loc", "seq_lens",
+        "block_table", "slot_mapping", "window", "sinks", "causal", "partition"]
+    written = [a.name for a in schema.arguments if a.alias_info and a.alias_info.is_write]
+    assert written == ["kv_member"]
+    schema8 = torch.ops.kvpath.paged_attention_fp8.default._schema
+    assert [a.name for a in schema8.arguments if a.alias_info and a.alias_info.is_write] == [
+        "kv_member", "kv_scale"]
 
 
 def _samples(fp8: bool) -> list[tuple]:
@@ -90,11 +104,17 @@ def test_opcheck(fp8) -> None:
 
 
 @pytest.mark.gpu
-def test_backward_through_the_op_raises() -> None:
-    """q requiring grad: the forward runs, `.backward()` raises NotImplementedError."""
-    args = step_args(DECODE, "cuda", torch.bfloat16)
+@pytest.mark.parametrize("fp8", [False, True])
+def test_backward_through_the_op_raises(fp8) -> None:
+    """q requiring grad: the forward runs (and bumps kv_member's version, an in-place write), the
+    output requires grad, and `.backward()` raises NotImplementedError naming the op."""
+    step = synthetic(DECODE, "cuda", torch.bfloat16, seed=77, pool_pages=128,
+                     cache_dtype=torch.float8_e4m3fn if fp8 else None)
+    args = step.args
     q = args[0].detach().requires_grad_(True)
-    out = kvpath.paged_attention(q, *args[1:])
-    assert out.requires_grad
+    version = args[3]._version
+    out = (kvpath.paged_attention_fp8(q, *args[1:], step.kv_scale) if fp8 else
+           kvpath.paged_attention(q, *args[1:]))
+    assert out.requires_grad and args[3]._version > version
     with pytest.raises(NotImplementedError, match="no backward"):
         out.float().sum().backward()
