@@ -117,7 +117,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         raise RuntimeError(
             f"libkvpath.so not found at {where}: build it first "
             f"(python -c 'import __graft_entry__ as g; g.build()' at the repo root, or "
-            f"python -m kvpath.build from research-2_amd/)")
+            f"python research-2_amd/kvpath/build.py)")
     lib = ctypes.CDLL(str(where))
     p = ctypes.POINTER
     i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p

@@ -2,7 +2,10 @@
 in-tree next to this file (kvpath/libkvpath.so), where `kvpath._lib` loads it; then
 libkvpath_torch.so, the torch.ops.kvpath registrations over its C ABI (csrc/kvpath_torch.cpp).
 
-    python -m kvpath.build          # from research-2_amd/, or via __graft_entry__.build()
+    python research-2_amd/kvpath/build.py     # or via __graft_entry__.build()
+
+The recipe imports nothing of the kvpath package (whose import loads the libraries it builds):
+__graft_entry__ loads this file by path, and the ISA scan next to it the same way.
 
 Each source is also compiled to gfx950 assembly with the same flags, and the assembly is scanned
 (kvpath.isa_scan) for any instruction that touches a register an inline-asm load may still be
@@ -76,9 +79,22 @@ class IsaHazardError(RuntimeError):
     """The assembly has an instruction that touches an outstanding inline-asm load's register."""
 
 
+def _isa_scan():
+    """kvpath/isa_scan.py, loaded by path (no package import)."""
+    import importlib.util
+
+    name = "kvpath_isa_scan"
+    if name not in sys.modules:
+        spec = importlib.util.spec_from_file_location(name, PACKAGE / "isa_scan.py")
+        module = importlib.util.module_from_spec(spec)
+        sys.modules[name] = module  # its dataclasses resolve their module through sys.modules
+        spec.loader.exec_module(module)
+    return sys.modules[name]
+
+
 def refuse_hazards(assembly: dict[str, str]) -> None:
     """Scan each source's assembly ({name: text}); raise IsaHazardError on any report."""
-    from kvpath import isa_scan
+    isa_scan = _isa_scan()
 
     found = {}
     for name, text in assembly.items():
