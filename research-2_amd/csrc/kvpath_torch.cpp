@@ -1,6 +1,8 @@
-// torch.ops.kvpath.paged_attention and paged_attention_fp8: kelpie's op
-// (kelpie/kelpie-models/kelpie_models/kernels/ops/paged_attention.py:67-140) registered with the
-// torch dispatcher in C++, over the C ABI of libkvpath.so (include/kvpath.h).
+// torch.ops.kvpath.paged_attention and paged_attention_fp8 -- kelpie's op
+// (kelpie/kelpie-models/kelpie_models/kernels/ops/paged_attention.py:67-140) -- and write_kv /
+// write_kv_fp8 (its append, :44-54, which DFlash's context injection also calls,
+// models/torch/dflash.py:197), registered with the torch dispatcher in C++ over the C ABI of
+// libkvpath.so (include/kvpath.h).
 //
 // An eager call from Python then costs the dispatcher's argument handling plus this file's
 // checks and one C-ABI call, with no Python frame between the caller and the launch (kelpie runs
@@ -218,6 +220,44 @@ at::Tensor paged_attention_fp8_hip(const at::Tensor& q, const at::Tensor& k, con
                                &kv_scale, partition);
 }
 
+// write_kv (kernels/ops/paged_attention.py:44-54): k, v [T, Hkv, D] into the member at the flat
+// slots, converted to the cache dtype; an fp8 member quantizes on append and updates kv_scale.
+void write_kv_any(const at::Tensor& kv_member, const at::Tensor& k, const at::Tensor& v,
+                  const at::Tensor& slot_mapping, const at::Tensor* kv_scale) {
+    const at::Device dev = one_device({&kv_member, &k, &v, &slot_mapping});
+    const kvpath_cache cache = cache_of(kv_member, kv_scale);
+    at::Tensor kk, vk, slot_k;
+    kvpath_rows kr = rows_of(k, "k", kk), vr = rows_of(v, "v", vk);
+    kvpath_plan plan{};
+    plan.slot_mapping = plan_ptr(slot_mapping, "slot_mapping", slot_k);
+    plan.num_tokens = k.size(0);
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(dev.index()).stream();
+    check(kvpath_kv_append(&cache, &kr, &vr, &plan, reinterpret_cast<kvpath_stream_t>(stream)),
+          "kv_append");
+}
+
+void write_kv_hip(at::Tensor& kv_member, const at::Tensor& k, const at::Tensor& v,
+                  const at::Tensor& slot_mapping) {
+    write_kv_any(kv_member, k, v, slot_mapping, nullptr);
+}
+
+void write_kv_fp8_hip(at::Tensor& kv_member, const at::Tensor& k, const at::Tensor& v,
+                      const at::Tensor& slot_mapping, at::Tensor& kv_scale) {
+    one_device({&kv_member, &kv_scale});
+    write_kv_any(kv_member, k, v, slot_mapping, &kv_scale);
+}
+
+void write_kv_cpu(at::Tensor& kv_member, const at::Tensor&, const at::Tensor&, const at::Tensor&) {
+    TORCH_CHECK(false, "kvpath: every tensor must be on one ROCm device, got ", kv_member.device(),
+                "; there is no CPU path");
+}
+
+void write_kv_fp8_cpu(at::Tensor& kv_member, const at::Tensor&, const at::Tensor&,
+                      const at::Tensor&, at::Tensor&) {
+    TORCH_CHECK(false, "kvpath: every tensor must be on one ROCm device, got ", kv_member.device(),
+                "; there is no CPU path");
+}
+
 // CPU tensors (dispatched here when no argument is on a ROCm device): refused, as the Python
 // layer refused them.
 at::Tensor paged_attention_cpu(const at::Tensor& q, const at::Tensor&, const at::Tensor&,
@@ -326,6 +366,9 @@ TORCH_LIBRARY(kvpath, m) {
           "Tensor row_request, Tensor positions, Tensor query_start_loc, Tensor seq_lens, "
           "Tensor block_table, Tensor slot_mapping, int window, Tensor sinks, bool causal, "
           "Tensor(a13!) kv_scale, int partition=0) -> Tensor");
+    m.def("write_kv(Tensor(a!) kv_member, Tensor k, Tensor v, Tensor slot_mapping) -> ()");
+    m.def("write_kv_fp8(Tensor(a!) kv_member, Tensor k, Tensor v, Tensor slot_mapping, "
+          "Tensor(b!) kv_scale) -> ()");
     m.def("plan_status_word(int device) -> Tensor", plan_status_word);
     m.def("set_check_slots(bool on) -> bool", set_check_slots);
 }
@@ -333,14 +376,51 @@ TORCH_LIBRARY(kvpath, m) {
 TORCH_LIBRARY_IMPL(kvpath, CUDA, m) {
     m.impl("paged_attention", paged_attention_hip);
     m.impl("paged_attention_fp8", paged_attention_fp8_hip);
+    m.impl("write_kv", write_kv_hip);
+    m.impl("write_kv_fp8", write_kv_fp8_hip);
 }
 
 TORCH_LIBRARY_IMPL(kvpath, CPU, m) {
     m.impl("paged_attention", paged_attention_cpu);
     m.impl("paged_attention_fp8", paged_attention_fp8_cpu);
+    m.impl("write_kv", write_kv_cpu);
+    m.impl("write_kv_fp8", write_kv_fp8_cpu);
 }
+
+namespace {
+
+// write_kv only writes its cache (no output to differentiate): below autograd, with the written
+// tensors' versions bumped as in-place writes.
+void write_kv_autograd(at::Tensor& kv_member, const at::Tensor& k, const at::Tensor& v,
+                       const at::Tensor& slot_mapping) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("kvpath::write_kv", "")
+                         .typed<decltype(write_kv_hip)>();
+    {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        op.call(kv_member, k, v, slot_mapping);
+    }
+    torch::autograd::impl::bump_version(kv_member);
+}
+
+void write_kv_fp8_autograd(at::Tensor& kv_member, const at::Tensor& k, const at::Tensor& v,
+                           const at::Tensor& slot_mapping, at::Tensor& kv_scale) {
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("kvpath::write_kv_fp8", "")
+                         .typed<decltype(write_kv_fp8_hip)>();
+    {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        op.call(kv_member, k, v, slot_mapping, kv_scale);
+    }
+    torch::autograd::impl::bump_version(kv_member);
+    torch::autograd::impl::bump_version(kv_scale);
+}
+
+}  // namespace
 
 TORCH_LIBRARY_IMPL(kvpath, Autograd, m) {
     m.impl("paged_attention", paged_attention_autograd);
     m.impl("paged_attention_fp8", paged_attention_fp8_autograd);
+    m.impl("write_kv", write_kv_autograd);
+    m.impl("write_kv_fp8", write_kv_fp8_autograd);
 }

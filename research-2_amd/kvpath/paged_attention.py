@@ -301,17 +301,24 @@ def workspace_bytes_max(max_tokens: int, max_reqs: int, n_heads: int, kv_heads: 
 def write_kv(kv_member: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              slot_mapping: torch.Tensor, kv_scale: torch.Tensor | None = None) -> None:
     """Scatter k, v [T, Hkv, D] into the member at flat slots (ops/paged_attention.py:44-54),
-    converting to the cache dtype; with an fp8 member, quantize on append and update kv_scale."""
-    dev = _on_device(kv_member, k, v, slot_mapping)
-    lib = _lib.load()
-    cache = _cache(kv_member, kv_scale)
-    kr, kk = _rows(k, "k")
-    vr, vv = _rows(v, "v")
-    plan, keep = _plan(None, None, None, None, slot_mapping, k.shape[0])
-    _lib.check("kv_append", lib.kvpath_kv_append(ctypes.byref(cache), ctypes.byref(kr),
-                                                   ctypes.byref(vr), ctypes.byref(plan),
-                                                   _stream(dev)))
-    del kk, vv, keep
+    converting to the cache dtype; with an fp8 member, quantize on append and update kv_scale.
+    (torch.ops.kvpath.write_kv / write_kv_fp8, registered in C++ over kvpath_kv_append.)"""
+    if kv_member.dtype == torch.float8_e4m3fn:
+        if kv_scale is None:
+            raise ValueError("kvpath: an fp8 kv_member needs kv_scale (new_kv_scale)")
+        torch.ops.kvpath.write_kv_fp8(kv_member, k, v, slot_mapping, kv_scale)
+    else:
+        torch.ops.kvpath.write_kv(kv_member, k, v, slot_mapping)
+
+
+@torch.library.register_fake("kvpath::write_kv")
+def _fake_write_kv(kv_member, k, v, slot_mapping):
+    del kv_member, k, v, slot_mapping
+
+
+@torch.library.register_fake("kvpath::write_kv_fp8")
+def _fake_write_kv_fp8(kv_member, k, v, slot_mapping, kv_scale):
+    del kv_member, k, v, slot_mapping, kv_scale
 
 
 def attend(q: torch.Tensor, kv_member: torch.Tensor, row_request: torch.Tensor,

@@ -419,8 +419,9 @@ def _check_against_oracle(out: torch.Tensor, args_gpu: tuple, entries: list[int]
 def test_config_attention(cfg) -> None:
     """Each BASELINE configuration (1-5), each workload of the callers next to the path
     (6 chunked prefill, 7/8 gpt-oss full and sliding-window decode with sinks, 9 the DFlash
-    drafter's non-causal block), and config 2 at 4096 keys (10), at its real shape (pool, heads, context lengths) through the
-    whole op, checked against the fp64 oracle on a subset of its entries."""
+    drafter's non-causal block), and config 2 at 4096 keys (10), at its real shape (pool,
+    heads, context lengths) through the whole op, checked against the fp64 oracle on every
+    entry (config 4: every fourth)."""
     batch, extra = config_batch(cfg)
     say("config", cfg, "entries", len(batch.entries))
     step = synthetic(batch, "cuda", extra["dtype"], seed=cfg, pool_pages=extra["pool_pages"],
@@ -434,8 +435,9 @@ def test_config_attention(cfg) -> None:
         atol, rtol = (BF16_ATOL, BF16_RTOL) if extra["dtype"] == torch.bfloat16 else (1e-4, 1e-4)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
-    subset = {1: None, 2: [0, 1, 17, 40, 63], 3: [0, 5, 15], 4: [0, 64, 127], 5: [2],
-              6: [0, 3], 7: [0, 31, 63], 8: [0, 31, 63], 9: [0, 7, 15], 10: [0, 31, 63]}[cfg]
+    # Every entry of every configuration, but config 4's every fourth (32 of 128: its pages,
+    # dequantized to fp64 for the oracle, are ~10 GB for all of them).
+    subset = list(range(0, 128, 4)) if cfg == 4 else None
     _check_against_oracle(out, args, subset, atol, rtol, step.kv_scale, f"config {cfg}")
 
 

@@ -45,12 +45,14 @@ def test_fake_shape_rule(batch) -> None:
 
 
 def test_ops_are_registered_for_every_key_they_need() -> None:
-    """Both ops (registered in C++, libkvpath_torch.so) have a ROCm kernel, a CPU kernel that
-    refuses, an Autograd kernel (whose backward raises, exercised on the GPU below) and a fake;
-    the schema is kelpie's 13 arguments with kv_member (and kv_scale) the only ones written."""
+    """The ops (registered in C++, libkvpath_torch.so: paged attention and write_kv, each plain
+    and fp8) have a ROCm kernel, a CPU kernel that refuses, an Autograd kernel (the attention
+    ops' backward raises, exercised on the GPU below) and a fake; the attention schema is
+    kelpie's 13 arguments with kv_member (and kv_scale) the only ones written."""
     from torch._library.simple_registry import singleton
 
-    for name in ("kvpath::paged_attention", "kvpath::paged_attention_fp8"):
+    for name in ("kvpath::paged_attention", "kvpath::paged_attention_fp8", "kvpath::write_kv",
+                 "kvpath::write_kv_fp8"):
         for key in ("CUDA", "CPU", "Autograd"):
             assert torch._C._dispatch_has_kernel_for_dispatch_key(name, key), (name, key)
         assert singleton.find(name).fake_impl.kernel is not None, name
