@@ -490,6 +490,7 @@ def measure(cfg: int, args, *, extras: bool) -> dict:
         app = []
         for st in rots:
             free = st.free_pages.cpu()
+            assert free.numel() >= n_pages, (free.numel(), n_pages)
             pages = free[torch.randperm(free.numel(), generator=g)[:n_pages]].to(torch.int64)
             slot_t = (pages[:, None] * batch.block + torch.arange(batch.block)).reshape(-1)
             kk = torch.randn(APPEND_ROWS, batch.kv_heads, batch.head_dim, device="cuda").to(dtype)

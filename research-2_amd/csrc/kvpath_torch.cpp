@@ -17,6 +17,7 @@
 // raises NotImplementedError.
 #include <ATen/ATen.h>
 #include <c10/hip/HIPException.h>
+#include <c10/hip/HIPGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/function.h>
 #include <torch/csrc/autograd/functions/utils.h>
@@ -106,6 +107,30 @@ const int32_t* plan_ptr(const at::Tensor& t, const char* what, at::Tensor& keep,
     return keep.data_ptr<int32_t>();
 }
 
+// The plan's lengths (kelpie's contract, ops/paged_attention.py:90-101): row_request, positions
+// and slot_mapping i32[T], query_start_loc i32[R+1], seq_lens i32[R], block_table i32[R, P]. The
+// kernels read them through bare pointers, so a tensor of another length is refused here instead
+// of being read past its end.
+void check_rows_of_plan(const at::Tensor& t, const char* what, int64_t T) {
+    TORCH_CHECK_VALUE(t.dim() == 1 && t.size(0) == T, "kvpath: ", what, " must be i32[T = ", T,
+                      "], got ", t.sizes());
+}
+
+void check_plan_lengths(int64_t T, const at::Tensor& row_request, const at::Tensor& positions,
+                        const at::Tensor& query_start_loc, const at::Tensor& seq_lens,
+                        const at::Tensor& block_table, const at::Tensor& slot_mapping) {
+    check_rows_of_plan(row_request, "row_request", T);
+    check_rows_of_plan(positions, "positions", T);
+    check_rows_of_plan(slot_mapping, "slot_mapping", T);
+    TORCH_CHECK_VALUE(seq_lens.dim() == 1, "kvpath: seq_lens must be i32[R], got ", seq_lens.sizes());
+    const int64_t R = seq_lens.size(0);
+    TORCH_CHECK_VALUE(query_start_loc.dim() == 1 && query_start_loc.size(0) == R + 1,
+                      "kvpath: query_start_loc must be i32[R + 1 = ", R + 1, "], got ",
+                      query_start_loc.sizes());
+    TORCH_CHECK_VALUE(block_table.dim() == 2 && block_table.size(0) == R,
+                      "kvpath: block_table must be i32[R = ", R, ", P], got ", block_table.sizes());
+}
+
 // One plan-status word per device (an int32 the kernels' plan check ORs 1 into), created zeroed
 // by the first call on the device outside stream capture and kept for the process; a call
 // captured before it exists passes none (its bad rows are still written as NaN). The tensors
@@ -148,10 +173,12 @@ at::Tensor paged_attention_any(const at::Tensor& q, const at::Tensor& k, const a
                                int64_t partition) {
     const at::Device dev = one_device({&q, &k, &v, &kv_member, &row_request, &positions,
                                        &query_start_loc, &seq_lens, &block_table, &slot_mapping});
+    const c10::hip::HIPGuard device_guard(dev.index());
     const kvpath_cache cache = cache_of(kv_member, kv_scale);
     at::Tensor qk, kk, vk;
     kvpath_rows qr = rows_of(q, "q", qk), kr = rows_of(k, "k", kk), vr = rows_of(v, "v", vk);
     const int64_t T = q.size(0), H = q.size(1), D = q.size(2);
+    check_plan_lengths(T, row_request, positions, query_start_loc, seq_lens, block_table, slot_mapping);
     at::Tensor out = at::empty({T, H * D}, q.options());
     kvpath_rows outr{out.data_ptr(), T, H, D, out.stride(0), D, dtype_code(out, "out")};
     at::Tensor rr_k, pos_k, qsl_k, len_k, table_k, slot_k;
@@ -225,9 +252,11 @@ at::Tensor paged_attention_fp8_hip(const at::Tensor& q, const at::Tensor& k, con
 void write_kv_any(const at::Tensor& kv_member, const at::Tensor& k, const at::Tensor& v,
                   const at::Tensor& slot_mapping, const at::Tensor* kv_scale) {
     const at::Device dev = one_device({&kv_member, &k, &v, &slot_mapping});
+    const c10::hip::HIPGuard device_guard(dev.index());
     const kvpath_cache cache = cache_of(kv_member, kv_scale);
     at::Tensor kk, vk, slot_k;
     kvpath_rows kr = rows_of(k, "k", kk), vr = rows_of(v, "v", vk);
+    check_rows_of_plan(slot_mapping, "slot_mapping", k.size(0));
     kvpath_plan plan{};
     plan.slot_mapping = plan_ptr(slot_mapping, "slot_mapping", slot_k);
     plan.num_tokens = k.size(0);

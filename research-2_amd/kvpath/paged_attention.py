@@ -21,9 +21,9 @@ nothing synchronizes and nothing traps, so the check sits in captured steps too.
 
 The two ops, torch.ops.kvpath.paged_attention and paged_attention_fp8, are registered in C++
 (csrc/kvpath_torch.cpp, built into libkvpath_torch.so beside libkvpath.so): the dispatcher calls
-the C ABI with no Python frame between the caller and the launch. Their fake (meta) rules are
-registered here. The other entry points (write_kv, attend, kv_gather, copy_blocks) bind the C
-ABI through ctypes (_lib).
+the C ABI with no Python frame between the caller and the launch; so are write_kv and
+write_kv_fp8, which `write_kv` calls. Their fake (meta) rules are registered here. The other
+entry points (attend, kv_gather, copy_blocks) bind the C ABI through ctypes (_lib).
 """
 
 from __future__ import annotations
@@ -173,6 +173,23 @@ def _plan(row_request, query_start_loc, seq_lens, block_table, slot_mapping, n_t
     def ptr(t: torch.Tensor | None) -> int | None:
         return None if t is None else t.data_ptr()
 
+    # The plan's lengths (ops/paged_attention.py:90-101): the kernels read these tensors through
+    # bare pointers, so one of another length is refused instead of being read past its end.
+    for t, what in ((row_request, "row_request"), (positions, "positions"),
+                    (slot_mapping, "slot_mapping")):
+        if t is not None and (t.dim() != 1 or t.shape[0] != n_tokens):
+            raise ValueError(f"kvpath: {what} must be i32[T = {n_tokens}], got {tuple(t.shape)}")
+    if seq_lens is not None:
+        if seq_lens.dim() != 1:
+            raise ValueError(f"kvpath: seq_lens must be i32[R], got {tuple(seq_lens.shape)}")
+        n = seq_lens.shape[0]
+        if query_start_loc is not None and (query_start_loc.dim() != 1 or
+                                            query_start_loc.shape[0] != n + 1):
+            raise ValueError(f"kvpath: query_start_loc must be i32[R + 1 = {n + 1}], got "
+                             f"{tuple(query_start_loc.shape)}")
+        if block_table is not None and (block_table.dim() != 2 or block_table.shape[0] != n):
+            raise ValueError(f"kvpath: block_table must be i32[R = {n}, P], got "
+                             f"{tuple(block_table.shape)}")
     table = i32(block_table, "block_table")
     n_reqs = seq_lens.shape[0] if seq_lens is not None else 0
     width = table.shape[1] if table is not None else 0
@@ -341,10 +358,11 @@ def attend(q: torch.Tensor, kv_member: torch.Tensor, row_request: torch.Tensor,
     opts, sinks = _opts(window, sinks, n_heads, causal, max(0, int(partition)))
     ws = _workspace(dev, n_tokens, seq_lens.shape[0], n_heads, kv_member.shape[3], head_dim,
                     block_table.shape[1], kv_member.shape[2], max(0, int(partition)))
-    _lib.check("attend", lib.kvpath_attend(ctypes.byref(qr), ctypes.byref(cache),
-                                           ctypes.byref(plan), ctypes.byref(opts),
-                                           ctypes.byref(outr), ws.data_ptr(), ws.numel(),
-                                           _stream(dev)))
+    with torch.cuda.device(dev):
+        _lib.check("attend", lib.kvpath_attend(ctypes.byref(qr), ctypes.byref(cache),
+                                               ctypes.byref(plan), ctypes.byref(opts),
+                                               ctypes.byref(outr), ws.data_ptr(), ws.numel(),
+                                               _stream(dev)))
     del qq, keep
     return out
 
@@ -394,8 +412,10 @@ def kv_gather(kv_member: torch.Tensor, block_table: torch.Tensor, width: int | N
     out_k = torch.empty(block_table.shape[0], width * block, heads, dim, dtype=kv_member.dtype,
                         device=dev)
     out_v = torch.empty_like(out_k)
-    _lib.check("kv_gather", lib.kvpath_kv_gather(ctypes.byref(cache), ctypes.byref(plan), width,
-                                                 out_k.data_ptr(), out_v.data_ptr(), _stream(dev)))
+    with torch.cuda.device(dev):
+        _lib.check("kv_gather", lib.kvpath_kv_gather(ctypes.byref(cache), ctypes.byref(plan), width,
+                                                     out_k.data_ptr(), out_v.data_ptr(),
+                                                     _stream(dev)))
     del keep
     return out_k, out_v
 
@@ -412,5 +432,7 @@ def copy_blocks(kv_member: torch.Tensor, src: torch.Tensor, dst: torch.Tensor,
         raise ValueError("kvpath: copy_blocks page ids must be int32")
     src, dst = src.contiguous(), dst.contiguous()
     cache = _cache(kv_member, kv_scale)
-    _lib.check("copy_blocks", lib.kvpath_copy_blocks(ctypes.byref(cache), src.data_ptr(),
-                                                     dst.data_ptr(), src.shape[0], _stream(dev)))
+    with torch.cuda.device(dev):
+        _lib.check("copy_blocks", lib.kvpath_copy_blocks(ctypes.byref(cache), src.data_ptr(),
+                                                         dst.data_ptr(), src.shape[0],
+                                                         _stream(dev)))

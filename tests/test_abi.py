@@ -313,3 +313,30 @@ def test_workspace_bound_covers_every_smaller_step(lib) -> None:
         prev = b
     assert bound(-1, 4, *shape) == -1 and bound(4, 4, 30, 8, 128, 64, 16, 0) == -1
     assert kvpath.workspace_bytes_max(64, 64, 32, 8, 128, 8192, 16) == bound(64, 64, *shape)
+
+
+def test_plan_lengths_are_checked() -> None:
+    """The plan's tensors reach the kernels as bare pointers, so one of another length than the
+    contract's (row_request, positions, slot_mapping i32[T]; query_start_loc i32[R+1]; block_table
+    i32[R, P]) is refused on the host, before anything reads past its end."""
+    import importlib
+
+    from workloads import Batch, step_args
+
+    pa = importlib.import_module("kvpath.paged_attention")  # the module (kvpath.paged_attention is the op)
+    batch = Batch(entries=((16, 1), (63, 4), (5, 16)), tokens=24, reqs=4, heads=8, kv_heads=2,
+                  head_dim=32, block=16)
+    args = step_args(batch, "cpu", torch.float32, seed=3)
+    rr, pos, qsl, lens, table, slots = (args[i] for i in (4, 5, 6, 7, 8, 9))
+    T = rr.shape[0]
+    pa._plan(rr, qsl, lens, table, slots, T, pos)  # the valid plan
+    cases = {
+        "row_request": (rr[:-1], qsl, lens, table, slots, pos),
+        "positions": (rr, qsl, lens, table, slots, pos[:-1]),
+        "slot_mapping": (rr, qsl, lens, table, slots[:-1], pos),
+        "query_start_loc": (rr, qsl[:-1], lens, table, slots, pos),
+        "block_table": (rr, qsl, lens, table[:-1], slots, pos),
+    }
+    for what, (a, b, c, d, e, f) in cases.items():
+        with pytest.raises(ValueError, match=what):
+            pa._plan(a, b, c, d, e, T, f)

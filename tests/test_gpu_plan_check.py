@@ -145,3 +145,31 @@ def test_valid_plans_keep_the_status_clear() -> None:
     finally:
         kvpath.set_slot_check(old)
     assert kvpath.plan_status() == 0
+
+
+def test_plan_lengths_are_refused_before_any_launch() -> None:
+    """The C++ ops check the plan's lengths on the host: a plan tensor shorter or longer than the
+    contract's raises ValueError naming it, and nothing is launched (the cache and the status
+    word are untouched)."""
+    batch, _ = SHAPES["decode_split"]
+    step = synthetic(batch, "cuda", torch.bfloat16, seed=7, pool_pages=2048)
+    args = list(step.args)
+    arena0 = step.arena.clone()
+    kvpath.clear_plan_status()
+    rr, pos, qsl, lens, table, slots = (args[i] for i in (4, 5, 6, 7, 8, 9))
+    cases = {
+        "row_request": (4, rr[:-1]),
+        "positions": (5, torch.cat([pos, pos[:1]])),
+        "query_start_loc": (6, qsl[:-1]),
+        "block_table": (8, table[:-1]),
+        "slot_mapping": (9, slots[:-1]),
+    }
+    for what, (i, bad) in cases.items():
+        say("plan length", what, tuple(bad.shape))
+        with pytest.raises(ValueError, match=what):
+            kvpath.paged_attention(*(args[:i] + [bad] + args[i + 1:]))
+    with pytest.raises(ValueError, match="slot_mapping"):
+        kvpath.write_kv(step.kv_member, args[1], args[2], slots[:-1])
+    torch.cuda.synchronize()
+    assert torch.equal(step.arena, arena0)
+    assert kvpath.plan_status() == 0

@@ -253,7 +253,8 @@ def config_batch(cfg: int, seed: int = 0) -> tuple[Batch, dict]:
         lens = uniform(128, 2048, 8192)
         b = Batch(entries=tuple((n - 1, 1) for n in lens), tokens=128, reqs=128, **llama)
         need = sum(math.ceil(n / 16) for n in lens)
-        return b, dict(pool_pages=need + 4096, dtype=torch.bfloat16,
+        # 4096 free pages beside the context's and the null page (the fp8 append step's pages)
+        return b, dict(pool_pages=need + 4096 + 1, dtype=torch.bfloat16,
                        cache_dtype=torch.float8_e4m3fn, outliers=0.01)
     if cfg == 5:
         b = Batch(entries=tuple((131072 - 1, 1) for _ in range(4)), tokens=4, reqs=4,
