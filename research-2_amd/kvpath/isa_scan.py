@@ -259,6 +259,13 @@ def scan(asm: str) -> dict[str, list[str]]:
                     lgkm = lgkm + ((False, frozenset()),)
                 # The hardware counters hold at most 63 vector / 15 LDS operations.
                 vm, lgkm = vm[-63:], lgkm[-15:]
+                # LDS-queue entries older than its oldest inline-asm read with a destination can
+                # neither be reported nor change which of the newer ones a wait retires (a wait
+                # keeps the newest N), and no rule reads this queue's length: drop them, so paths
+                # that differ only in such entries (the compiler's scalar loads, LDS stores) meet
+                # in one state. (The vector queue keeps its length: the wait pairs read it.)
+                while lgkm and not lgkm[0][1]:
+                    lgkm = lgkm[1:]
                 _track_constants(ins, consts)
             pair = _wait_pair(blocks, bi)
             if pair is not None:
