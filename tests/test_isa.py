@@ -170,6 +170,46 @@ def test_scanner_takes_a_wait_pair_as_one_wait() -> None:
     assert any("v0, v6" in r for r in scan(other_flag)["_Zkernel"])
 
 
+def test_scanner_merges_paths_that_differ_in_register_less_lds_entries(monkeypatch) -> None:
+    """The LDS queue's entries older than its oldest inline-asm read carry nothing to report and
+    cannot change which reads a wait retires, so the scan drops them: a read behind a scalar load
+    and an LDS store is still reported when used early; a register-less entry issued after the
+    read still counts for lgkmcnt(N); and paths that differ only in such entries meet in one
+    state (a chain of twelve optional scalar loads scans within 100 block visits, where keeping
+    every queue length apart takes several hundred)."""
+    early = """_Zkernel: ; @k
+\ts_load_dword s0, s[2:3], 0x0
+\tds_write_b32 v1, v2
+\t;;#ASMSTART
+\tds_read_b128 v[6:9], v10
+\t;;#ASMEND
+\tv_mov_b32_e32 v0, v6
+\ts_waitcnt lgkmcnt(0)
+\ts_endpgm
+"""
+    reports = scan(early)["_Zkernel"]
+    assert len(reports) == 1 and "v0, v6" in reports[0]
+    newer = """_Zkernel: ; @k
+\t;;#ASMSTART
+\tds_read_b128 v[6:9], v10
+\t;;#ASMEND
+\tds_write_b32 v1, v2
+\ts_waitcnt lgkmcnt(1)
+\tv_mov_b32_e32 v0, v6
+\ts_endpgm
+"""
+    assert not scan(newer)["_Zkernel"]
+    assert scan(newer.replace("lgkmcnt(1)", "lgkmcnt(2)"))["_Zkernel"]
+    chain = ["_Zkernel: ; @k"]
+    for i in range(12):
+        chain += [f"\ts_cmp_lt_i32 s4, {i}", f"\ts_cbranch_scc1 .LBB0_{i}",
+                  f"; %bb.x{i}:", f"\ts_load_dword s{10 + i}, s[2:3], 0x{4 * i:x}", f".LBB0_{i}:"]
+    chain += ["\t;;#ASMSTART", "\tds_read_b128 v[6:9], v10", "\t;;#ASMEND", "\ts_waitcnt lgkmcnt(0)",
+              "\tv_mov_b32_e32 v0, v6", "\ts_endpgm", ""]
+    monkeypatch.setattr("kvpath.isa_scan._MAX_VISITS", 100)
+    assert not scan("\n".join(chain))["_Zkernel"]
+
+
 def test_build_refuses_a_hazard() -> None:
     """kvpath.build.build() scans the assembly before linking: a report raises."""
     build.refuse_hazards({"clean.s": BACK_EDGE.replace(
