@@ -315,15 +315,6 @@ template <bool BF16P>
 __device__ __forceinline__ float partial_scale(float l) { return BF16P ? l : 1.0f; }
 
 typedef short v4s __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4s lds_v4s;
-
-// Four bf16 of a staged V tile, transposed across the lane group (ds_read_b64_tr_b16): lane
-// 4a + b of each 16-lane group receives element b of the 8-byte rows addressed by lanes a,
-// a + 4, a + 8, a + 12 of its group.
-__device__ __forceinline__ v4s lds_read_tr16(const uint16_t* p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<lds_v4s*>(reinterpret_cast<uintptr_t>(p) & 0xffffffffu));
-}
 
 // The online softmax keeps each q-row's running max m and rescales its accumulators only when a
 // block's max exceeds m by more than kRescaleLog2 (log2 units); probabilities 2^(s - m) then stay
@@ -390,9 +381,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
-// ds_read_b64_tr_b16 (see lds_read_tr16) that the compiler does not track: it would otherwise
-// wait for every outstanding global_load_lds before the first LDS read (it cannot tell which
-// LDS bytes they write). The caller waits (wait_lds_ops) and passes the result through
+// Four bf16 of a staged V tile, transposed across the lane group (ds_read_b64_tr_b16): lane
+// 4a + b of each 16-lane group receives element b of the 8-byte rows addressed by lanes a,
+// a + 4, a + 8, a + 12 of its group. Issued as inline asm the compiler does not track: it would
+// otherwise wait for every outstanding global_load_lds before the first LDS read (it cannot tell
+// which LDS bytes they write). The caller waits (wait_lds_ops) and passes the result through
 // after_wait() before use.
 __device__ __forceinline__ v4s lds_read_tr16_async(uint32_t addr) {
     v4s v;
